@@ -1,0 +1,134 @@
+/*
+ * rhinoforge_amd -- W8A16 weight-only quantized linear for MI355X (gfx950).
+ *
+ * C ABI of the drop-in boundary.  Plain pointers and sizes only: no torch or
+ * HIP types appear in the signatures (a HIP stream is passed as `void*`,
+ * NULL = the null stream).  Every entry point returns an rf_w8a16_status;
+ * nothing is ever silently computed on the CPU.
+ *
+ * Operation:  y[M,N] = x[M,K] . (s[N] (.) q[N,K])^T (+ b[N])
+ *   x, y, s, b : fp16 (IEEE binary16, little-endian), y accumulated in fp32
+ *   q          : int8 per-output-channel weights, packed by rf_w8a16_pack_weight
+ *
+ * Reference interfaces (paths relative to the RhinoForge tree):
+ *   - W8A16 launchers: src/ops/rpu_linear.cpp:1047-1209 (tiled GEMM branch,
+ *     declared src/core/rpu_kernel_decls.h:1083-1101) and
+ *     src/ops/rpu_linear_gemv.cpp:46-202 (llama_gemv_wint8, declared
+ *     src/core/rpu_kernel_decls.h:1120-1127);
+ *   - weight swizzle: python/rpu_backend/runtime/weights.py:150-233 and its
+ *     C++ twin src/ops/rpu_linear.cpp:67-131;
+ *   - tile / kernel selection: src/ops/rpu_linear_tiling.h:544-595 and the
+ *     M==1 GEMV hand-off src/ops/rpu_linear.cpp:1094-1103.
+ */
+#ifndef RHINOFORGE_AMD_W8A16_H_
+#define RHINOFORGE_AMD_W8A16_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RF_W8A16_ABI_VERSION 1
+
+/* Status codes.  The torch op maps each to a RuntimeError with the message
+ * from rf_w8a16_status_str (the reference raises TORCH_CHECK before any
+ * launch, e.g. src/ops/rpu_linear.cpp:1120-1134). */
+typedef enum rf_w8a16_status {
+  RF_W8A16_OK = 0,
+  RF_W8A16_EINVAL = 1,      /* bad shape, size or null pointer            */
+  RF_W8A16_EALIGN = 2,      /* pointer or leading-dimension alignment     */
+  RF_W8A16_ELAYOUT = 3,     /* weight layout tag not accepted             */
+  RF_W8A16_EWORKSPACE = 4,  /* workspace missing or too small             */
+  RF_W8A16_EHIP = 5,        /* HIP runtime error (launch or query)        */
+  RF_W8A16_EDEVICE = 6,     /* current device is not gfx950               */
+  RF_W8A16_EKERNEL = 7      /* requested kernel cannot run this shape     */
+} rf_w8a16_status;
+
+/* Weight layout tags (the analogue of the reference's `partition` record,
+ * python/rpu_backend/runtime/weights.py:33-51, 386-408).
+ *
+ * RF_W8A16_LAYOUT_ROWMAJOR: q[N,K] int8 row-major, the on-disk checkpoint
+ *   format written by quant/convert_qwen3.py:65-100.  Never accepted by the
+ *   compute entry point: pack it first.
+ * RF_W8A16_LAYOUT_TILE16X64: the CDNA4 tile order.  With Np = ceil(N/16)*16
+ *   and Kp = ceil(K/64)*64 the buffer holds Np*Kp bytes as 1024-byte tiles,
+ *   tile (nb, kb) at byte offset (nb*(Kp/64) + kb)*1024; inside a tile the
+ *   16 bytes at offset 16*l (l = 0..63) are
+ *       q[16*nb + l%16][64*kb + 16*(l/16) + j] XOR 0x80,   j = 0..15
+ *   (XOR 0x80 stores q+128 as an unsigned byte); padding rows/columns hold
+ *   q = 0.  One tile is exactly one wavefront-wide 128-bit load, and the 16
+ *   bytes of lane l are that lane's two fp16 MFMA B operands.
+ */
+#define RF_W8A16_LAYOUT_ROWMAJOR 0
+#define RF_W8A16_LAYOUT_TILE16X64 1
+
+/* Kernel choice (the analogue of `force_gemm`, rpu_linear.cpp:1094-1103). */
+#define RF_W8A16_KERNEL_AUTO 0
+#define RF_W8A16_KERNEL_GEMV 1 /* decode GEMV / skinny GEMM, M <= 64       */
+#define RF_W8A16_KERNEL_GEMM 2 /* LDS-staged dequant-into-MFMA GEMM         */
+
+/* Human-readable text for a status code; never NULL. */
+const char* rf_w8a16_status_str(int status);
+
+/* ABI version of the loaded library (RF_W8A16_ABI_VERSION). */
+int rf_w8a16_abi_version(void);
+
+/* Bytes of a TILE16X64-packed weight for an [N,K] matrix; 0 if N<1 or K<1. */
+size_t rf_w8a16_packed_bytes(int64_t N, int64_t K);
+
+/* Host repack: row-major q[N,K] (row stride ldq >= K bytes) -> TILE16X64.
+ * Replaces tp_col_swizzle_mc_weight / tp_row_swizzle_mc_weight /
+ * transform_linear_weight (runtime/weights.py:150-233; rpu_linear.cpp:67-131).
+ * Exact and invertible (see rf_w8a16_unpack_weight). */
+int rf_w8a16_pack_weight(const int8_t* q, int64_t N, int64_t K, int64_t ldq,
+                         void* dst, size_t dst_bytes);
+
+/* Host inverse of rf_w8a16_pack_weight (tests and checkpoint export). */
+int rf_w8a16_unpack_weight(const void* packed, int64_t N, int64_t K,
+                           int8_t* q, int64_t ldq);
+
+/* Device repack on `stream`: q_dev row-major in device memory -> dst_dev.
+ * Same result as rf_w8a16_pack_weight; used at load time so multi-hundred-MB
+ * weights (e.g. a 151936x5120 lm_head) never round-trip through the host. */
+int rf_w8a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K,
+                                int64_t ldq, void* dst_dev, size_t dst_bytes,
+                                void* stream);
+
+/* Kernel the AUTO policy runs for this shape on the current device
+ * (RF_W8A16_KERNEL_GEMV or RF_W8A16_KERNEL_GEMM), or a negative status. */
+int rf_w8a16_select_kernel(int64_t M, int64_t N, int64_t K);
+
+/* Workspace bytes rf_w8a16_linear needs for (M,N,K) with any kernel choice
+ * on the current device.  The first RF_W8A16_WS_COUNTER_BYTES bytes are
+ * split-K arrival counters: they must be zero before the first call that
+ * uses the buffer, and every successful call leaves them zero again. */
+size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
+#define RF_W8A16_WS_COUNTER_BYTES 65536
+
+/* y = x . dequant(w)^T (+ bias), on `stream` (asynchronous).
+ *   x        : fp16 [M, ldx], 16-byte aligned, ldx % 8 == 0, ldx >= K
+ *   w_packed : rf_w8a16_packed_bytes(N,K) bytes in `layout` (TILE16X64)
+ *   scale    : fp16 [N], per-output-channel scale
+ *   bias     : fp16 [N] or NULL; added once after the K reduction
+ *              (rpu_linear.cpp:279-283, 796-808)
+ *   y        : fp16 [M, ldy], ldy >= N
+ *   M >= 1, N >= 1, K >= 8, K % 8 == 0
+ *   kernel   : RF_W8A16_KERNEL_AUTO / _GEMV / _GEMM
+ *   workspace: device buffer of >= rf_w8a16_workspace_bytes(M,N,K) bytes,
+ *              counters zeroed as described above; calls that share one
+ *              workspace must be ordered (same stream).
+ * Replaces rpu_launch_linear_spm_to_spm_acc16_kernel (rpu_linear.cpp:1047)
+ * and rpu_launch_gemv_spm_to_spm_kernel (rpu_linear_gemv.cpp:46). */
+int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed,
+                    int32_t layout, const void* scale, const void* bias,
+                    void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                    int32_t kernel, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* RHINOFORGE_AMD_W8A16_H_ */

@@ -1,0 +1,80 @@
+"""ctypes binding of the C ABI in include/w8a16.h.
+
+This is the binding a Python host (such as the reference's runtime) would add
+to call the library without the torch op.  It loads ``lib/librf_w8a16.so``;
+import torch first in processes that use the GPU, so that the HIP runtime
+torch ships is the one the library binds to.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "librf_w8a16.so"
+
+OK = 0
+EINVAL = 1
+EALIGN = 2
+ELAYOUT = 3
+EWORKSPACE = 4
+EHIP = 5
+EDEVICE = 6
+EKERNEL = 7
+LAYOUT_ROWMAJOR = 0
+LAYOUT_TILE16X64 = 1
+KERNEL_AUTO = 0
+KERNEL_GEMV = 1
+KERNEL_GEMM = 2
+WS_COUNTER_BYTES = 65536
+
+# name -> (restype, argtypes): every entry point declared in include/w8a16.h
+_c = ctypes
+SIGNATURES = {
+    "rf_w8a16_status_str": (_c.c_char_p, [_c.c_int]),
+    "rf_w8a16_abi_version": (_c.c_int, []),
+    "rf_w8a16_packed_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64]),
+    "rf_w8a16_pack_weight": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
+                                        _c.c_void_p, _c.c_size_t]),
+    "rf_w8a16_unpack_weight": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p,
+                                          _c.c_int64]),
+    "rf_w8a16_pack_weight_device": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
+                                               _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "rf_w8a16_select_kernel": (_c.c_int, [_c.c_int64, _c.c_int64, _c.c_int64]),
+    "rf_w8a16_workspace_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int64]),
+    "rf_w8a16_linear": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int32,
+                                   _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64,
+                                   _c.c_int64, _c.c_int64, _c.c_int64, _c.c_int32,
+                                   _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the C-ABI library (once) and declare every signature."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.is_file():
+            raise OSError(f"{LIB_PATH} not built; run `python -m rhinoforge_amd._build`")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+class W8A16Error(RuntimeError):
+    def __init__(self, status: int, what: str) -> None:
+        self.status = status
+        super().__init__(f"{what}: {status_str(status)} (status {status})")
+
+
+def status_str(status: int) -> str:
+    return load().rf_w8a16_status_str(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        raise W8A16Error(status, what)

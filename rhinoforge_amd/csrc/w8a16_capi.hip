@@ -1,0 +1,259 @@
+// C-ABI layer: validation, kernel choice, workspace sizing, weight packing.
+//
+// Validation mirrors the reference launchers' TORCH_CHECKs
+// (src/ops/rpu_linear.cpp:1119-1134 -- int8 [N,K] weight, fp16 [N] scale,
+// byte extents; src/ops/rpu_linear_gemv.cpp:105-123 -- scale.numel()==N,
+// alignment) but returns status codes; the torch op turns them into errors.
+// Unlike the RPU the kernels accept every M, N >= 1 and K % 8 == 0: there is
+// no core partition to satisfy (runtime/weights.py:97-135), only the
+// 16-byte activation-row alignment of a 128-bit load.
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/w8a16.h"
+#include "w8a16_common.h"
+#include "w8a16_internal.h"
+
+namespace rf {
+
+// ---------------------------------------------------------------------------
+// Device properties, cached per device (read-only after the first query).
+// ---------------------------------------------------------------------------
+int device_info(DeviceInfo* out) {
+  static std::mutex mu;
+  static std::vector<int> state;  // 0 = unknown, 1 = cached
+  static std::vector<DeviceInfo> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return RF_W8A16_EHIP;
+  std::lock_guard<std::mutex> g(mu);
+  if ((int)state.size() <= dev) {
+    state.resize(dev + 1, 0);
+    cache.resize(dev + 1);
+  }
+  if (!state[dev]) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return RF_W8A16_EHIP;
+    DeviceInfo d;
+    d.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    d.gfx950 = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    cache[dev] = d;
+    state[dev] = 1;
+  }
+  *out = cache[dev];
+  return RF_W8A16_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Device repack kernel: one thread per 16-byte lane chunk of a tile.
+// ---------------------------------------------------------------------------
+namespace {
+__global__ void pack_kernel(const int8_t* __restrict__ q, int64_t N, int64_t K, int64_t ldq,
+                            uint8_t* __restrict__ dst, int64_t kblocks, int64_t chunks) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= chunks) return;
+  const int64_t tile = idx >> 6;
+  const int lane = (int)(idx & 63);
+  const int64_t nb = tile / kblocks, kb = tile % kblocks;
+  const int64_t n = nb * 16 + (lane & 15);
+  const int64_t k0 = kb * 64 + 16 * (lane >> 4);
+  uint32_t words[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int64_t k = k0 + w * 4 + b;
+      const uint8_t qb = (n < N && k < K) ? (uint8_t)q[n * ldq + k] : 0u;
+      v |= (uint32_t)(uint8_t)(qb ^ 0x80u) << (8 * b);
+    }
+    words[w] = v;
+  }
+  *reinterpret_cast<uint4*>(dst + idx * 16) = make_uint4(words[0], words[1], words[2], words[3]);
+}
+}  // namespace
+
+hipError_t launch_pack(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* dst,
+                       hipStream_t stream) {
+  const int64_t kblocks = ceil_div(K, 64);
+  const int64_t chunks = ceil_div(N, 16) * kblocks * 64;
+  const int64_t blocks = ceil_div(chunks, 256);
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, q, N, K, ldq, dst,
+                     kblocks, chunks);
+  return hipGetLastError();
+}
+
+}  // namespace rf
+
+using rf::ceil_div;
+using rf::round_up;
+
+namespace {
+
+constexpr int64_t kMaxDim = (int64_t)1 << 30;
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_nk(int64_t N, int64_t K) {
+  if (N < 1 || K < 1 || N > kMaxDim || K > kMaxDim) return RF_W8A16_EINVAL;
+  return RF_W8A16_OK;
+}
+
+// Kernel the AUTO policy picks; GEMV covers M <= 64, the GEMM everything.
+int auto_kernel(int64_t M) { return M <= 64 ? RF_W8A16_KERNEL_GEMV : RF_W8A16_KERNEL_GEMM; }
+
+}  // namespace
+
+extern "C" {
+
+const char* rf_w8a16_status_str(int status) {
+  switch (status) {
+    case RF_W8A16_OK: return "ok";
+    case RF_W8A16_EINVAL: return "invalid argument (shape, size or null pointer)";
+    case RF_W8A16_EALIGN:
+      return "misaligned operand (x must be 16-byte aligned with ldx % 8 == 0 and K % 8 == 0)";
+    case RF_W8A16_ELAYOUT:
+      return "weight layout not accepted: pack the row-major int8 weight with "
+             "rf_w8a16_pack_weight (layout TILE16X64) first";
+    case RF_W8A16_EWORKSPACE: return "workspace missing or smaller than rf_w8a16_workspace_bytes()";
+    case RF_W8A16_EHIP: return "HIP runtime error";
+    case RF_W8A16_EDEVICE: return "current HIP device is not gfx950 (MI355X)";
+    case RF_W8A16_EKERNEL: return "requested kernel cannot run this shape";
+    default: return "unknown rf_w8a16 status";
+  }
+}
+
+int rf_w8a16_abi_version(void) { return RF_W8A16_ABI_VERSION; }
+
+size_t rf_w8a16_packed_bytes(int64_t N, int64_t K) {
+  if (check_nk(N, K) != RF_W8A16_OK) return 0;
+  return (size_t)round_up(N, 16) * (size_t)round_up(K, 64);
+}
+
+int rf_w8a16_pack_weight(const int8_t* q, int64_t N, int64_t K, int64_t ldq, void* dst,
+                         size_t dst_bytes) {
+  if (check_nk(N, K) != RF_W8A16_OK || !q || !dst || ldq < K) return RF_W8A16_EINVAL;
+  if (dst_bytes < rf_w8a16_packed_bytes(N, K)) return RF_W8A16_EINVAL;
+  const int64_t kblocks = ceil_div(K, 64), nstrips = ceil_div(N, 16);
+  uint8_t* out = static_cast<uint8_t*>(dst);
+  for (int64_t nb = 0; nb < nstrips; ++nb) {
+    for (int64_t kb = 0; kb < kblocks; ++kb) {
+      uint8_t* tile = out + (nb * kblocks + kb) * 1024;
+      for (int l = 0; l < 64; ++l) {
+        const int64_t n = nb * 16 + (l & 15);
+        const int64_t k0 = kb * 64 + 16 * (l >> 4);
+        for (int j = 0; j < 16; ++j) {
+          const int64_t k = k0 + j;
+          const uint8_t qb = (n < N && k < K) ? (uint8_t)q[n * ldq + k] : 0u;
+          tile[l * 16 + j] = (uint8_t)(qb ^ 0x80u);
+        }
+      }
+    }
+  }
+  return RF_W8A16_OK;
+}
+
+int rf_w8a16_unpack_weight(const void* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq) {
+  if (check_nk(N, K) != RF_W8A16_OK || !packed || !q || ldq < K) return RF_W8A16_EINVAL;
+  const int64_t kblocks = ceil_div(K, 64);
+  const uint8_t* in = static_cast<const uint8_t*>(packed);
+  for (int64_t n = 0; n < N; ++n) {
+    const int64_t nb = n >> 4;
+    const int nl = (int)(n & 15);
+    for (int64_t k = 0; k < K; ++k) {
+      const int64_t kb = k >> 6;
+      const int kk = (int)(k & 63);
+      const int l = nl + 16 * (kk >> 4);
+      q[n * ldq + k] = (int8_t)(in[(nb * kblocks + kb) * 1024 + l * 16 + (kk & 15)] ^ 0x80u);
+    }
+  }
+  return RF_W8A16_OK;
+}
+
+int rf_w8a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K, int64_t ldq,
+                                void* dst_dev, size_t dst_bytes, void* stream) {
+  if (check_nk(N, K) != RF_W8A16_OK || !q_dev || !dst_dev || ldq < K) return RF_W8A16_EINVAL;
+  if (dst_bytes < rf_w8a16_packed_bytes(N, K)) return RF_W8A16_EINVAL;
+  if (!aligned(dst_dev, 16)) return RF_W8A16_EALIGN;
+  hipError_t e = rf::launch_pack(q_dev, N, K, ldq, static_cast<uint8_t*>(dst_dev),
+                                 static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
+}
+
+int rf_w8a16_select_kernel(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return -RF_W8A16_EINVAL;
+  return auto_kernel(M);
+}
+
+size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return 0;
+  size_t bytes = RF_W8A16_WS_COUNTER_BYTES;
+  if (M <= 64) {
+    rf::DeviceInfo dev;
+    if (rf::device_info(&dev) != RF_W8A16_OK) {
+      dev.cus = 256;
+      dev.gfx950 = false;
+    }
+    const rf::GemvPlan p = rf::plan_gemv((int)M, (int)N, (int)K, dev);
+    bytes += rf::gemv_workspace_bytes(p, (int)M, (int)N);
+  }
+  return bytes;
+}
+
+int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed, int32_t layout,
+                    const void* scale, const void* bias, void* y, int64_t ldy, int64_t M,
+                    int64_t N, int64_t K, int32_t kernel, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (!x || !w_packed || !scale || !y) return RF_W8A16_EINVAL;
+  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return RF_W8A16_EINVAL;
+  if (ldx < K || ldy < N) return RF_W8A16_EINVAL;
+  if (layout != RF_W8A16_LAYOUT_TILE16X64) return RF_W8A16_ELAYOUT;
+  if (K % 8 != 0 || ldx % 8 != 0 || !aligned(x, 16)) return RF_W8A16_EALIGN;
+  if (!aligned(w_packed, 16) || !aligned(scale, 2) || !aligned(y, 2) ||
+      (bias && !aligned(bias, 2)))
+    return RF_W8A16_EALIGN;
+  if ((N + 15) / 16 > 0x7fffffff / 1 || (K + 63) / 64 > 0x7fffffff) return RF_W8A16_EINVAL;
+
+  rf::DeviceInfo dev;
+  int st = rf::device_info(&dev);
+  if (st != RF_W8A16_OK) return st;
+  if (!dev.gfx950) return RF_W8A16_EDEVICE;
+
+  if (kernel == RF_W8A16_KERNEL_AUTO) kernel = auto_kernel(M);
+  if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
+  if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
+
+  rf::LinearArgs a;
+  a.x = static_cast<const _Float16*>(x);
+  a.ldx = ldx;
+  a.w = static_cast<const uint8_t*>(w_packed);
+  a.scale = static_cast<const _Float16*>(scale);
+  a.bias = static_cast<const _Float16*>(bias);
+  a.y = static_cast<_Float16*>(y);
+  a.ldy = ldy;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.kblocks = (int)ceil_div(K, 64);
+  a.nstrips = (int)ceil_div(N, 16);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  hipError_t e;
+  if (kernel == RF_W8A16_KERNEL_GEMV) {
+    const rf::GemvPlan p = rf::plan_gemv(a.M, a.N, a.K, dev);
+    if (p.splits > 1) {
+      const size_t need = RF_W8A16_WS_COUNTER_BYTES + rf::gemv_workspace_bytes(p, a.M, a.N);
+      if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+        return RF_W8A16_EWORKSPACE;
+    }
+    e = rf::launch_gemv(a, p, p.splits > 1 ? workspace : nullptr, s);
+  } else {
+    const rf::GemmPlan p = rf::plan_gemm(a.M, a.N, a.K, dev);
+    e = rf::launch_gemm(a, p, s);
+  }
+  return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,74 @@
+// Device-side building blocks shared by the W8A16 kernels (gfx950 / CDNA4).
+//
+// Weight tiles use the TILE16X64 layout declared in include/w8a16.h: one
+// 1024-byte tile = 16 output channels x 64 input channels, lane l of a
+// wavefront owns the 16 bytes at offset 16*l, holding q+128 for channel
+// l%16 and input positions 16*(l/16) .. 16*(l/16)+15 of the tile.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rf {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileN = 16;       // output channels per tile
+constexpr int kTileK = 64;       // input channels per tile
+constexpr int kTileBytes = 1024; // kTileN * kTileK
+constexpr int kWave = 64;
+
+// Exact int8 -> fp16 for the four bytes of `d` (each byte u = q + 128).
+//
+// v_perm_b32 places each byte u under the fp16 exponent byte 0x64, giving
+// the fp16 number 1024 + u (exact: integers up to 2048 are representable);
+// one packed fp16 subtraction of 1152 = 1024 + 128 then yields q exactly.
+// This is the "magic number" conversion (Kim et al. 2022, "Who says
+// elephants can't run", int8 -> fp16 via exponent bias), written for
+// v_perm_b32 + v_pk_add_f16.  Four VALU ops per four weights.
+__device__ __forceinline__ half4 dequant4(uint32_t d) {
+  const uint32_t exp_bytes = 0x64646464u;
+  // perm selector bytes: 0..3 pick bytes of `d`, 4..7 pick bytes of exp_bytes
+  const uint32_t lo = __builtin_amdgcn_perm(exp_bytes, d, 0x04010400u);  // [u0 | 0x64, u1 | 0x64]
+  const uint32_t hi = __builtin_amdgcn_perm(exp_bytes, d, 0x04030402u);  // [u2 | 0x64, u3 | 0x64]
+  const half2v off = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const half2v a = __builtin_bit_cast(half2v, lo) - off;
+  const half2v b = __builtin_bit_cast(half2v, hi) - off;
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3);
+}
+
+// Eight weights (two dwords, in memory order) -> one fp16 MFMA operand.
+__device__ __forceinline__ half8 dequant8(uint32_t d0, uint32_t d1) {
+  return __builtin_shufflevector(dequant4(d0), dequant4(d1), 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// D(16x16, fp32) += A(16x32, fp16) * B(32x16, fp16).
+// Lane l supplies A row l%16 and B column l%16, each for the 8 K positions
+// of k-group l/16; the product pairs A and B slots with the same (group,
+// slot), so any consistent K assignment of the operands gives the same sum.
+// Result: lane l, element r holds D[4*(l/16) + r][l%16].
+__device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint4 load_u4(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// Streaming (read-once) 128-bit load: weights are touched exactly once per
+// call, so they are marked non-temporal to keep L2 for activations/partials.
+__device__ __forceinline__ uint4 load_u4_stream(const void* p) {
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ half8 as_half8(uint4 v) {
+  return __builtin_bit_cast(half8, v);
+}
+
+}  // namespace rf

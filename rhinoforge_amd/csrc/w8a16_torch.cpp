@@ -1,0 +1,255 @@
+// Thin torch-library op over the rf_w8a16 C ABI (PyTorch-ROCm).
+//
+// Schemas (namespace `w8a16`):
+//   linear(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias=None,
+//          int layout=1, int kernel=0) -> Tensor
+//   linear_into(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias,
+//               Tensor(a!) out, int layout=1, int kernel=0) -> ()
+//   pack_weight(Tensor q) -> Tensor
+//   unpack_weight(Tensor packed, int N, int K) -> Tensor
+//   select_kernel(int M, int N, int K) -> int
+//
+// These mirror the reference's eager FP16 `linear_into` (schema at
+// src/core/rpu_dispatch_registrations.inc:19-20, checks at
+// src/ops/rpu_linear.cpp:664-731) with the fp16 per-channel scale carried
+// next to the int8 weight as in `causal_decoder_set_lm_head`
+// (registrations :46): input [..., K] is flattened to [M, K]
+// (rpu_linear.cpp:596-613), weight is int8 in the packed layout, scale fp16
+// [N], bias fp16 [N] added once after the reduction.  Invalid input raises;
+// there is no CPU compute path and no silent fallback (the reference also
+// refuses to run swizzled weights on the CPU, rpu_linear.cpp:193-196).
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "../../include/w8a16.h"
+
+namespace {
+
+void check_status(int st, const char* what) {
+  TORCH_CHECK(st == RF_W8A16_OK, what, ": ", rf_w8a16_status_str(st), " (status ", st, ")");
+}
+
+int64_t ceil_to(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
+
+// Workspace per (device, stream): allocated through torch's caching
+// allocator, zero-filled once (fill kernel), grown on demand.  The C ABI
+// leaves its counter region zero after every call, and calls on one stream
+// are ordered, so one buffer per stream is safe to reuse.
+struct WorkspaceCache {
+  std::mutex mu;
+  std::map<std::pair<int, void*>, at::Tensor> bufs;
+
+  at::Tensor get(const at::Device& dev, void* stream, size_t bytes) {
+    std::lock_guard<std::mutex> g(mu);
+    auto key = std::make_pair((int)dev.index(), stream);
+    auto it = bufs.find(key);
+    if (it != bufs.end() && (size_t)it->second.numel() >= bytes) return it->second;
+    const int64_t sz = ceil_to((int64_t)std::max<size_t>(bytes, 1 << 20), 1 << 20);
+    at::Tensor t = at::zeros({sz}, at::TensorOptions().dtype(at::kByte).device(dev));
+    bufs[key] = t;
+    return t;
+  }
+};
+
+WorkspaceCache& workspace_cache() {
+  static WorkspaceCache* c = new WorkspaceCache();  // lives until process exit
+  return *c;
+}
+
+struct Checked {
+  at::Tensor x2;  // [M, K] view/copy with 16-byte aligned rows
+  int64_t M, N, K;
+};
+
+Checked check_args(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                   const c10::optional<at::Tensor>& bias, int64_t layout, const char* op) {
+  TORCH_CHECK(input.scalar_type() == at::kHalf, op, ": input must be float16, got ",
+              input.scalar_type());
+  TORCH_CHECK(weight.scalar_type() == at::kChar, op,
+              ": weight must be int8 (W8A16 packed weight), got ", weight.scalar_type());
+  TORCH_CHECK(scale.scalar_type() == at::kHalf, op, ": weight_scale must be float16, got ",
+              scale.scalar_type());
+  TORCH_CHECK(input.dim() >= 1, op, ": input must have at least one dimension");
+  TORCH_CHECK(layout == RF_W8A16_LAYOUT_TILE16X64, op, ": layout ", layout,
+              " not accepted: ", rf_w8a16_status_str(RF_W8A16_ELAYOUT));
+  TORCH_CHECK(input.is_cuda() && weight.is_cuda() && scale.is_cuda(), op,
+              ": input, weight and weight_scale must be on a HIP device (there is no CPU "
+              "implementation)");
+  TORCH_CHECK(input.device() == weight.device() && input.device() == scale.device(), op,
+              ": input, weight and weight_scale must be on the same device");
+  TORCH_CHECK(scale.dim() == 1 && scale.is_contiguous(), op,
+              ": weight_scale must be a contiguous 1-D [N] tensor, got ", scale.sizes());
+  const int64_t N = scale.size(0);
+  const int64_t K = input.size(-1);
+  TORCH_CHECK(N >= 1, op, ": N (weight_scale.numel()) must be >= 1");
+  TORCH_CHECK(K >= 8 && K % 8 == 0, op, ": in_features K=", K, " must be a positive multiple of 8");
+  TORCH_CHECK(weight.is_contiguous() && weight.dim() == 2 && weight.size(0) == ceil_to(N, 16) &&
+                  weight.size(1) == ceil_to(K, 64),
+              op, ": packed weight must be contiguous int8 [", ceil_to(N, 16), ", ",
+              ceil_to(K, 64), "] for N=", N, ", K=", K, " (use w8a16.pack_weight), got ",
+              weight.sizes());
+  if (bias.has_value() && bias->defined()) {
+    const at::Tensor& b = *bias;
+    TORCH_CHECK(b.scalar_type() == at::kHalf, op, ": bias must be float16");
+    TORCH_CHECK(b.is_cuda() && b.device() == input.device(), op,
+                ": bias must be on the input's device");
+    TORCH_CHECK(b.dim() == 1 && b.size(0) == N && b.is_contiguous(), op,
+                ": bias must be a contiguous vector with ", N, " elements, got shape ",
+                b.sizes());
+  }
+  Checked c;
+  c.N = N;
+  c.K = K;
+  c.M = input.numel() / K;
+  at::Tensor x2 = input.reshape({c.M, K});
+  const bool ok = x2.stride(1) == 1 && x2.stride(0) % 8 == 0 &&
+                  (reinterpret_cast<uintptr_t>(x2.data_ptr()) % 16) == 0;
+  // Otherwise copy into a fresh (allocator-aligned) contiguous buffer.
+  c.x2 = ok ? x2 : (x2.is_contiguous() ? x2.clone() : x2.contiguous());
+  return c;
+}
+
+void launch(const Checked& c, const at::Tensor& weight, const at::Tensor& scale,
+            const c10::optional<at::Tensor>& bias, at::Tensor& y2, int64_t layout,
+            int64_t kernel, const char* op) {
+  if (c.M == 0) return;
+  c10::DeviceGuard guard(c.x2.device());
+  void* stream = c10::hip::getCurrentHIPStream(c.x2.device().index()).stream();
+  const size_t ws_bytes = rf_w8a16_workspace_bytes(c.M, c.N, c.K);
+  TORCH_CHECK(ws_bytes > 0, op, ": ", rf_w8a16_status_str(RF_W8A16_EINVAL));
+  at::Tensor ws = workspace_cache().get(c.x2.device(), stream, ws_bytes);
+  const void* bptr = (bias.has_value() && bias->defined()) ? bias->data_ptr() : nullptr;
+  const int st = rf_w8a16_linear(c.x2.data_ptr(), c.x2.stride(0), weight.data_ptr(), (int32_t)layout,
+                                 scale.data_ptr(), bptr, y2.data_ptr(), y2.stride(0), c.M, c.N,
+                                 c.K, (int32_t)kernel, ws.data_ptr(), (size_t)ws.numel(), stream);
+  check_status(st, op);
+}
+
+at::Tensor linear_hip(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                      const c10::optional<at::Tensor>& bias, int64_t layout, int64_t kernel) {
+  RECORD_FUNCTION("w8a16::linear", {});
+  Checked c = check_args(input, weight, scale, bias, layout, "w8a16::linear");
+  at::Tensor y2 = at::empty({c.M, c.N}, input.options());
+  launch(c, weight, scale, bias, y2, layout, kernel, "w8a16::linear");
+  std::vector<int64_t> shape = input.sizes().vec();
+  shape.back() = c.N;
+  return y2.view(shape);
+}
+
+void linear_into_hip(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                     const c10::optional<at::Tensor>& bias, at::Tensor& out, int64_t layout,
+                     int64_t kernel) {
+  RECORD_FUNCTION("w8a16::linear_into", {});
+  Checked c = check_args(input, weight, scale, bias, layout, "w8a16::linear_into");
+  TORCH_CHECK(out.scalar_type() == at::kHalf, "w8a16::linear_into: out must be float16");
+  TORCH_CHECK(out.is_cuda() && out.device() == input.device(),
+              "w8a16::linear_into: out must be on the input's device");
+  std::vector<int64_t> shape = input.sizes().vec();
+  shape.back() = c.N;
+  TORCH_CHECK(out.sizes() == shape, "w8a16::linear_into: out shape must be ", shape, ", got ",
+              out.sizes());
+  TORCH_CHECK(out.is_contiguous(), "w8a16::linear_into: out must be contiguous");
+  at::Tensor y2 = out.view({c.M, c.N});
+  launch(c, weight, scale, bias, y2, layout, kernel, "w8a16::linear_into");
+}
+
+at::Tensor linear_meta(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                       const c10::optional<at::Tensor>& bias, int64_t layout, int64_t kernel) {
+  std::vector<int64_t> shape = input.sizes().vec();
+  TORCH_CHECK(!shape.empty() && scale.dim() == 1, "w8a16::linear: bad shapes");
+  shape.back() = scale.size(0);
+  return at::empty(shape, input.options());
+}
+
+[[noreturn]] void no_cpu(const char* op) {
+  TORCH_CHECK(false, op,
+              ": tensors are on the CPU; the W8A16 kernels run on a HIP device (gfx950) only "
+              "and there is no CPU implementation");
+}
+
+at::Tensor linear_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                      const c10::optional<at::Tensor>&, int64_t, int64_t) {
+  no_cpu("w8a16::linear");
+}
+
+void linear_into_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                     const c10::optional<at::Tensor>&, at::Tensor&, int64_t, int64_t) {
+  no_cpu("w8a16::linear_into");
+}
+
+// Repack a row-major int8 [N, K] weight into the TILE16X64 layout.
+// CPU tensors are packed on the host, HIP tensors on the device.
+at::Tensor pack_weight(const at::Tensor& q) {
+  TORCH_CHECK(q.scalar_type() == at::kChar, "w8a16::pack_weight: q must be int8, got ",
+              q.scalar_type());
+  TORCH_CHECK(q.dim() == 2, "w8a16::pack_weight: q must be 2-D [N, K], got ", q.sizes());
+  const int64_t N = q.size(0), K = q.size(1);
+  TORCH_CHECK(N >= 1 && K >= 1, "w8a16::pack_weight: empty weight ", q.sizes());
+  at::Tensor qc = q.contiguous();
+  at::Tensor out = at::empty({ceil_to(N, 16), ceil_to(K, 64)}, q.options());
+  const size_t bytes = rf_w8a16_packed_bytes(N, K);
+  TORCH_CHECK((size_t)out.numel() == bytes, "w8a16::pack_weight: size mismatch");
+  if (q.is_cuda()) {
+    c10::DeviceGuard guard(q.device());
+    void* stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
+    check_status(rf_w8a16_pack_weight_device(qc.data_ptr<int8_t>(), N, K, K, out.data_ptr(), bytes,
+                                             stream),
+                 "w8a16::pack_weight");
+  } else {
+    TORCH_CHECK(q.device().is_cpu(), "w8a16::pack_weight: unsupported device ", q.device());
+    check_status(rf_w8a16_pack_weight(qc.data_ptr<int8_t>(), N, K, K, out.data_ptr(), bytes),
+                 "w8a16::pack_weight");
+  }
+  return out;
+}
+
+// Inverse of pack_weight (host); returns a CPU int8 [N, K] tensor.
+at::Tensor unpack_weight(const at::Tensor& packed, int64_t N, int64_t K) {
+  TORCH_CHECK(packed.scalar_type() == at::kChar, "w8a16::unpack_weight: packed must be int8");
+  TORCH_CHECK(N >= 1 && K >= 1, "w8a16::unpack_weight: N and K must be >= 1");
+  TORCH_CHECK(packed.numel() == (int64_t)rf_w8a16_packed_bytes(N, K),
+              "w8a16::unpack_weight: packed has ", packed.numel(), " bytes, expected ",
+              rf_w8a16_packed_bytes(N, K));
+  at::Tensor p = packed.to(at::kCPU).contiguous();
+  at::Tensor q = at::empty({N, K}, p.options());
+  check_status(rf_w8a16_unpack_weight(p.data_ptr(), N, K, q.data_ptr<int8_t>(), K),
+               "w8a16::unpack_weight");
+  return q;
+}
+
+int64_t select_kernel(int64_t M, int64_t N, int64_t K) {
+  const int k = rf_w8a16_select_kernel(M, N, K);
+  TORCH_CHECK(k > 0, "w8a16::select_kernel: ", rf_w8a16_status_str(-k));
+  return k;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(w8a16, m) {
+  m.def("linear(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias=None, "
+        "int layout=1, int kernel=0) -> Tensor");
+  m.def("linear_into(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias, "
+        "Tensor(a!) out, int layout=1, int kernel=0) -> ()");
+  m.def("pack_weight(Tensor q) -> Tensor", TORCH_FN(pack_weight));
+  m.def("unpack_weight(Tensor packed, int N, int K) -> Tensor", TORCH_FN(unpack_weight));
+  m.def("select_kernel(int M, int N, int K) -> int", TORCH_FN(select_kernel));
+}
+
+// HIP tensors carry the CUDA dispatch key on PyTorch-ROCm.
+TORCH_LIBRARY_IMPL(w8a16, CUDA, m) {
+  m.impl("linear", TORCH_FN(linear_hip));
+  m.impl("linear_into", TORCH_FN(linear_into_hip));
+}
+
+TORCH_LIBRARY_IMPL(w8a16, Meta, m) { m.impl("linear", TORCH_FN(linear_meta)); }
+
+TORCH_LIBRARY_IMPL(w8a16, CPU, m) {
+  m.impl("linear", TORCH_FN(linear_cpu));
+  m.impl("linear_into", TORCH_FN(linear_into_cpu));
+}

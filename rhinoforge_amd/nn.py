@@ -1,0 +1,74 @@
+"""``W8A16Linear``: an nn.Module holding a packed int8 weight and fp16 scale.
+
+The reference keeps ``nn.Linear`` modules with an int8 ``weight`` Parameter and
+an fp16 ``weight_scale`` buffer (python/rpu_backend/quant/load.py:267-284),
+swizzles the weight in place at load time and records the layout on the
+module (runtime/weights.py:386-408, 411-544).  Here the packed weight lives in
+a ``weight`` buffer of shape ``packed_shape(N, K)`` and the layout tag in
+``self.layout``; forward calls ``torch.ops.w8a16.linear``.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import ops
+from .quant import quantize_linear_per_channel
+
+
+class W8A16Linear(nn.Module):
+    def __init__(self, in_features: int, out_features: int, bias: bool = False,
+                 device=None) -> None:
+        super().__init__()
+        if in_features < 8 or in_features % 8:
+            raise ValueError(f"in_features={in_features} must be a positive multiple of 8")
+        if out_features < 1:
+            raise ValueError(f"out_features={out_features} must be >= 1")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.layout = ops.LAYOUT_TILE16X64
+        np_, kp = ops.packed_shape(out_features, in_features)
+        self.register_buffer("weight", torch.full((np_, kp), -128, dtype=torch.int8, device=device))
+        self.register_buffer("weight_scale", torch.ones(out_features, dtype=torch.float16,
+                                                        device=device))
+        if bias:
+            self.register_buffer("bias", torch.zeros(out_features, dtype=torch.float16,
+                                                     device=device))
+        else:
+            self.bias = None
+
+    @classmethod
+    def from_quantized(cls, q: torch.Tensor, weight_scale: torch.Tensor,
+                       bias: torch.Tensor | None = None) -> "W8A16Linear":
+        """From an on-disk pair: ``X.weight`` int8 [N, K] row-major and
+        ``X.weight_scale`` fp16 [N] (quant/convert_qwen3.py:65-100 format)."""
+        if q.dtype != torch.int8 or q.dim() != 2:
+            raise TypeError(f"weight must be int8 [N, K], got {q.dtype} {tuple(q.shape)}")
+        n, k = q.shape
+        if weight_scale.dtype != torch.float16 or tuple(weight_scale.shape) != (n,):
+            raise TypeError(f"weight_scale must be fp16 [{n}], got {weight_scale.dtype} "
+                            f"{tuple(weight_scale.shape)}")
+        mod = cls(k, n, bias=bias is not None, device="meta")
+        mod.weight = ops.pack_weight(q)
+        mod.weight_scale = weight_scale.contiguous()
+        if bias is not None:
+            mod.bias = bias.to(torch.float16).contiguous()
+        return mod
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear) -> "W8A16Linear":
+        """Quantize a floating nn.Linear per channel, then pack."""
+        q, s = quantize_linear_per_channel(linear.weight.detach())
+        b = linear.bias.detach().to(torch.float16) if linear.bias is not None else None
+        return cls.from_quantized(q, s, b)
+
+    def rowmajor_weight(self) -> torch.Tensor:
+        """The int8 [N, K] row-major weight (CPU), e.g. for checkpoint export."""
+        return ops.unpack_weight(self.weight, self.out_features, self.in_features)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return ops.linear(x, self.weight, self.weight_scale, self.bias, layout=self.layout)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, layout=TILE16X64")

@@ -1,0 +1,61 @@
+"""Python face of the ``torch.ops.w8a16`` op (see csrc/w8a16_torch.cpp).
+
+Call conventions follow the reference's eager ``linear_into``
+(src/core/rpu_dispatch_registrations.inc:19-20; src/ops/rpu_linear.cpp:664-731)
+with the fp16 scale next to the int8 weight, as in ``causal_decoder_set_lm_head``
+(registrations :46).  The ``layout`` argument is the analogue of the
+reference's recorded ``partition`` (python/rpu_backend/runtime/weights.py:386-408)
+and ``kernel`` the analogue of ``force_gemm`` (src/ops/rpu_linear.cpp:1094-1103).
+"""
+from __future__ import annotations
+
+import torch
+
+LAYOUT_ROWMAJOR = 0
+LAYOUT_TILE16X64 = 1
+KERNEL_AUTO = 0
+KERNEL_GEMV = 1
+KERNEL_GEMM = 2
+
+
+def packed_shape(n: int, k: int) -> tuple[int, int]:
+    """Shape of the packed int8 weight for a logical [n, k] weight."""
+    return ((n + 15) // 16 * 16, (k + 63) // 64 * 64)
+
+
+def pack_weight(q: torch.Tensor) -> torch.Tensor:
+    """Row-major int8 [N, K] -> TILE16X64 packed int8 [ceil16(N), ceil64(K)].
+
+    Replaces the reference's load-time swizzle ``transform_linear_weight``
+    (runtime/weights.py:206-233).  Runs on the device for HIP tensors and on
+    the host for CPU tensors; the on-disk checkpoint stays row-major.
+    """
+    return torch.ops.w8a16.pack_weight(q)
+
+
+def unpack_weight(packed: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """Inverse of :func:`pack_weight`; returns a CPU int8 [n, k] tensor."""
+    return torch.ops.w8a16.unpack_weight(packed, n, k)
+
+
+def linear(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+           bias: torch.Tensor | None = None, *, layout: int = LAYOUT_TILE16X64,
+           kernel: int = KERNEL_AUTO) -> torch.Tensor:
+    """y = input . (weight_scale (.) q)^T (+ bias), fp16 out, fp32 accumulation.
+
+    input [..., K] fp16; weight = pack_weight(q) for q int8 [N, K];
+    weight_scale fp16 [N]; bias fp16 [N] or None.  HIP tensors only.
+    """
+    return torch.ops.w8a16.linear(input, weight, weight_scale, bias, layout, kernel)
+
+
+def linear_into(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                bias: torch.Tensor | None, out: torch.Tensor, *,
+                layout: int = LAYOUT_TILE16X64, kernel: int = KERNEL_AUTO) -> None:
+    """In-place variant writing into a caller-owned contiguous ``out`` [..., N]."""
+    torch.ops.w8a16.linear_into(input, weight, weight_scale, bias, out, layout, kernel)
+
+
+def select_kernel(m: int, n: int, k: int) -> int:
+    """Kernel the AUTO policy runs for (M, N, K): KERNEL_GEMV or KERNEL_GEMM."""
+    return int(torch.ops.w8a16.select_kernel(m, n, k))

@@ -1,0 +1,352 @@
+"""GPU parity of the W8A16 kernels against the CPU oracle (MI355X only).
+
+Bar: max|y - y_cpu| <= 1e-2 * rms(y_cpu) and cosine(y, y*) >=
+0.9999 against the fp64 oracle, outputs finite.  y_cpu is the reference's
+dequantize-then-matmul CPU path (oracle.w8a16.cpu_path), y* the fp64 oracle.
+Exact-arithmetic cases (one-hot activations) are compared bit for bit.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import rhinoforge_amd as rf
+from rhinoforge_amd import capi
+from oracle import w8a16 as o
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = Path(__file__).resolve().parent / "golden"
+KERNELS = {"auto": rf.KERNEL_AUTO, "gemv": rf.KERNEL_GEMV, "gemm": rf.KERNEL_GEMM}
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+_WEIGHTS: dict = {}
+
+
+def make_weights(n, k, seed):
+    """(q, s) numpy.  Small weights come from the oracle's portable generator and
+    quantizer; large ones are drawn N(0, 0.02) on the GPU (torch, seeded) and
+    quantized there by the package quantizer (bit-exact with the oracle's, see
+    test_host.py and test_gpu_quantizer_matches_oracle)."""
+    key = (n, k, seed)
+    if key not in _WEIGHTS:
+        if n * k <= (1 << 22):
+            q, s = o.quantize_linear_per_channel(o.make_weight(o.derive_seed(seed, "w", n, k), n, k))
+        else:
+            g = torch.Generator(device=DEV).manual_seed(o.derive_seed(seed, "w", n, k) & 0x7FFFFFFF)
+            w = torch.randn(n, k, generator=g, device=DEV, dtype=torch.float32) * 0.02
+            qd, sd = rf.quantize_linear_per_channel(w)
+            q, s = qd.cpu().numpy(), sd.cpu().numpy()
+            del w, qd, sd
+        _WEIGHTS.clear()  # keep at most one large weight resident
+        _WEIGHTS[key] = (q, s)
+    return _WEIGHTS[key]
+
+
+def make_case(m, n, k, seed, *, bias=False, outlier=0.0, rmsn=False):
+    q, s = make_weights(n, k, seed)
+    x = o.make_activation(o.derive_seed(seed, "x", m, k), m, k, rms_normalize=rmsn,
+                          outlier_frac=outlier)
+    b = (o.normal(o.derive_seed(seed, "b", n), (n,)) * 0.1).astype(np.float16) if bias else None
+    return x, q, s, b
+
+
+def run_gpu(x, q, s, b, kernel=rf.KERNEL_AUTO, packed=None):
+    wp = packed if packed is not None else rf.pack_weight(_to_dev(q))
+    y = rf.linear(_to_dev(x), wp, _to_dev(s), None if b is None else _to_dev(b), kernel=kernel)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def assert_parity(y, x, q, s, b, rows=None, label=""):
+    xs = x if rows is None else x[rows]
+    ys = y if rows is None else y[rows]
+    y_cpu = o.cpu_path(xs, q, s, b)
+    y_star = o.oracle_fp64(xs, q, s, b)
+    rep = o.check_tolerance(ys, y_cpu, y_star)
+    _say(f"  {label}: {rep}")
+    assert rep.ok, f"{label}: {rep}"
+    return rep
+
+
+# ---------------------------------------------------------------- exactness
+@pytest.mark.parametrize("kernel,m", [("gemv", 1), ("gemv", 16), ("gemv", 40), ("gemm", 130)])
+def test_one_hot_rows_are_exact(kernel, m):
+    """x[r] = e_{k_r}: y[r, n] = fp16(s[n] * q[n, k_r]) exactly (one product, no sum)."""
+    n, k = 80, 200
+    _say(f"one-hot {kernel} M={m} N={n} K={k}")
+    rng = np.random.default_rng(m)
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (rng.random(n) * 0.05 + 1e-3).astype(np.float16)
+    ks = rng.integers(0, k, size=m)
+    x = np.zeros((m, k), np.float16)
+    x[np.arange(m), ks] = 1.0
+    y = run_gpu(x, q, s, None, KERNELS[kernel])
+    expect = o.dequantize_linear_per_channel(q, s)[:, ks].T
+    assert (y.view(np.uint16) == expect.view(np.uint16)).all()
+
+
+# ---------------------------------------------------------------- golden fixtures
+def _sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.mark.parametrize("kernel", sorted(KERNELS))
+@pytest.mark.parametrize("path", sorted(GOLDEN.glob("*.npz")), ids=lambda p: p.stem)
+def test_golden_fixtures(path, kernel):
+    rec = np.load(path)
+    name, n, k, seed = path.stem, int(rec["N"]), int(rec["K"]), int(rec["seed"])
+    w = o.make_weight(o.derive_seed(seed, name, "w"), n, k)
+    q, s = o.quantize_linear_per_channel(w)
+    b = ((o.normal(o.derive_seed(seed, name, "b"), (n,)) * 0.1).astype(np.float16)
+         if bool(rec["bias"]) else None)
+    packed = rf.pack_weight(_to_dev(q))
+    for m in (int(v) for v in rec["M_list"]):
+        if kernel == "gemv" and m > 64:
+            continue
+        x = o.make_activation(o.derive_seed(seed, name, "x", m), m, k,
+                              rms_normalize=bool(rec["rms_normalize"]),
+                              outlier_frac=float(rec["outlier_frac"]))
+        assert _sha(x) == str(rec[f"sha_x_{m}"])
+        _say(f"golden {name} {kernel} M={m}")
+        y = run_gpu(x, q, s, b, KERNELS[kernel], packed)
+        rep = o.check_tolerance(y, rec[f"y_cpu_{m}"], rec[f"y_star_{m}"])
+        assert rep.ok, f"{name} M={m} {kernel}: {rep}"
+
+
+# ---------------------------------------------------------------- BASELINE configs
+def test_cfg0_qwen3_06b_decode():
+    x, q, s, b = make_case(1, 3072, 1024, seed=0)
+    packed = rf.pack_weight(_to_dev(q))
+    for kern in ("auto", "gemv", "gemm"):
+        _say(f"cfg0 {kern}")
+        assert_parity(run_gpu(x, q, s, b, KERNELS[kern], packed), x, q, s, b, label=f"cfg0 {kern}")
+
+
+QWEN3_8B = {"q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+            "gate": (12288, 4096), "up": (12288, 4096), "down": (4096, 12288)}
+QWEN3_VL_32B = {"q": (8192, 5120), "k": (1024, 5120), "v": (1024, 5120), "o": (5120, 8192),
+                "gate": (25600, 5120), "up": (25600, 5120), "down": (5120, 25600)}
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_cfg1_qwen3_8b_decode_layer(m):
+    for proj, (n, k) in QWEN3_8B.items():
+        _say(f"cfg1 M={m} {proj} N={n} K={k}")
+        x, q, s, b = make_case(m, n, k, seed=1)
+        assert rf.select_kernel(m, n, k) == rf.KERNEL_GEMV
+        assert_parity(run_gpu(x, q, s, b), x, q, s, b, label=f"cfg1 M={m} {proj}")
+
+
+@pytest.mark.parametrize("m", [1, 32, 512])
+def test_cfg4_qwen3_vl_32b_projections(m):
+    for proj, (n, k) in QWEN3_VL_32B.items():
+        _say(f"cfg4 M={m} {proj} N={n} K={k}")
+        x, q, s, b = make_case(m, n, k, seed=4, outlier=0.01)
+        rows = None if m <= 32 else np.random.default_rng(m).choice(m, 96, replace=False)
+        assert_parity(run_gpu(x, q, s, b), x, q, s, b, rows=rows, label=f"cfg4 M={m} {proj}")
+
+
+def test_cfg3_qwen3_8b_prefill_mlp():
+    m = 2048
+    for proj in ("gate", "up", "down"):
+        n, k = QWEN3_8B[proj]
+        _say(f"cfg3 M={m} {proj} N={n} K={k}")
+        x, q, s, b = make_case(m, n, k, seed=3)
+        assert rf.select_kernel(m, n, k) == rf.KERNEL_GEMM
+        y = run_gpu(x, q, s, b)
+        rows = np.random.default_rng(3).choice(m, 128, replace=False)
+        assert_parity(y, x, q, s, b, rows=rows, label=f"cfg3 {proj} sampled rows")
+        # every row against an fp32 dequantize-then-matmul on the GPU (torch)
+        w32 = _to_dev(q).float() * _to_dev(s).float()[:, None]
+        ref = _to_dev(x).float() @ w32.T.contiguous()
+        yt = _to_dev(y).float()
+        rel = ((yt - ref).abs().max() / ref.pow(2).mean().sqrt()).item()
+        cos = torch.nn.functional.cosine_similarity(yt, ref, dim=1).min().item()
+        _say(f"  all rows vs torch fp32: err/rms={rel:.3g} min_row_cos={cos:.8f}")
+        assert rel <= 1e-2 and cos >= 0.9999
+
+
+def _lm_head_weights():
+    n, k = 151936, 5120
+    g = torch.Generator(device=DEV).manual_seed(14)
+    w = torch.randn(n, k, generator=g, device=DEV, dtype=torch.float32) * 0.02
+    q, s = rf.quantize_linear_per_channel(w)
+    del w
+    return q, s
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_cfg2_qwen3_14b_lm_head(m):
+    _say(f"cfg2 lm_head M={m}")
+    q_dev, s_dev = _lm_head_weights()
+    q, s = q_dev.cpu().numpy(), s_dev.cpu().numpy()
+    x = o.make_activation(o.derive_seed(2, "x", m), m, 5120, rms_normalize=True)
+    y = run_gpu(x, q, s, None, packed=rf.pack_weight(q_dev))
+    assert_parity(y, x, q, s, None, label=f"cfg2 M={m}")
+
+
+def test_cfg2_lm_head_argmax_agreement_1000_rows():
+    """Greedy-token agreement with the CPU path over 1000 seeded rows, with near-tie accounting
+    (a disagreement counts as a tie when the fp64 oracle's top-2 gap is below the output's
+    fp16 rounding, docs/validation_policy.md:124-128)."""
+    _say("cfg2 argmax 1000 rows")
+    q_dev, s_dev = _lm_head_weights()
+    packed = rf.pack_weight(q_dev)
+    x = o.make_activation(o.derive_seed(2, "argmax"), 1000, 5120, rms_normalize=True)
+    y = rf.linear(_to_dev(x), packed, s_dev)  # M=1000: GEMM
+    y8 = torch.cat([rf.linear(_to_dev(x[i:i + 8]), packed, s_dev) for i in range(0, 1000, 8)])
+    torch.cuda.synchronize()
+    # CPU path: fp16 dequantized weight, fp32 accumulation (adapters/qwen3.py:617-623)
+    w16 = o.dequantize_fp32_then_fp16(q_dev.cpu().numpy(), s_dev.cpu().numpy())
+    y_cpu = (x.astype(np.float32) @ w16.astype(np.float32).T).astype(np.float16)
+    a_cpu = y_cpu.astype(np.float32).argmax(1)
+    for label, yy in (("gemm M=1000", y), ("gemv M=8 batches", y8)):
+        a_gpu = yy.float().argmax(1).cpu().numpy()
+        bad = np.nonzero(a_gpu != a_cpu)[0]
+        ties = 0
+        for r in bad:
+            v_g = float(y_cpu[r, a_gpu[r]])
+            v_c = float(y_cpu[r, a_cpu[r]])
+            if abs(v_c - v_g) <= 2 * float(np.spacing(np.float16(abs(v_c)))):
+                ties += 1
+        _say(f"  {label}: agree {1000 - len(bad)}/1000, near-ties {ties}")
+        assert len(bad) - ties == 0
+
+
+# ---------------------------------------------------------------- edge cases
+EDGE = [(1, 1, 8), (1, 17, 72), (2, 100, 136), (16, 16, 64), (17, 33, 520), (33, 48, 1024),
+        (64, 80, 200), (65, 33, 520), (3, 5, 4104), (200, 130, 264), (1, 4000, 16)]
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("m,n,k", EDGE)
+def test_edge_shapes(m, n, k, bias):
+    _say(f"edge M={m} N={n} K={k} bias={bias}")
+    x, q, s, b = make_case(m, n, k, seed=11, bias=bias)
+    packed = rf.pack_weight(_to_dev(q))
+    kernels = ["auto", "gemm"] + (["gemv"] if m <= 64 else [])
+    for kern in kernels:
+        assert_parity(run_gpu(x, q, s, b, KERNELS[kern], packed), x, q, s, b,
+                      label=f"edge {m}x{n}x{k} {kern}")
+
+
+def test_zero_rows_and_extreme_scales():
+    n, k = 64, 256
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[0] = 0.0
+    w[1] *= 1e4
+    w[2] *= 1e-5
+    q, s = o.quantize_linear_per_channel(w)
+    x = o.make_activation(6, 4, k)
+    for kern in ("gemv", "gemm"):
+        y = run_gpu(x, q, s, None, KERNELS[kern])
+        assert (y[:, 0] == 0).all()
+        assert_parity(y, x, q, s, None, label=f"extreme scales {kern}")
+
+
+def test_split_k_deterministic_and_reusable():
+    """Small-N shapes take the split-K path; repeated calls are bitwise identical
+    (fixed reduction order) and keep working (counters are left zeroed)."""
+    x, q, s, b = make_case(4, 1024, 4096, seed=12)
+    packed = rf.pack_weight(_to_dev(q))
+    xd, sd = _to_dev(x), _to_dev(s)
+    first = rf.linear(xd, packed, sd)
+    for _ in range(50):
+        again = rf.linear(xd, packed, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    assert_parity(first.cpu().numpy(), x, q, s, b, label="split-K")
+
+
+def test_gpu_quantizer_matches_oracle():
+    w = o.make_weight(31, 300, 1000)
+    w[3] = 0
+    qd, sd = rf.quantize_linear_per_channel(_to_dev(w))
+    q, s = o.quantize_linear_per_channel(w)
+    assert (qd.cpu().numpy() == q).all()
+    assert (sd.cpu().numpy().view(np.uint16) == s.view(np.uint16)).all()
+
+
+def test_device_pack_equals_host_pack():
+    for n, k in [(17, 72), (3072, 1024), (100, 8)]:
+        q = torch.randint(-128, 128, (n, k), dtype=torch.int8)
+        assert torch.equal(rf.pack_weight(q.to(DEV)).cpu(), rf.pack_weight(q))
+
+
+def test_input_views_3d_empty_and_linear_into():
+    x, q, s, b = make_case(6, 96, 128, seed=13, bias=True)
+    packed, sd, bd = rf.pack_weight(_to_dev(q)), _to_dev(s), _to_dev(b)
+    ref = rf.linear(_to_dev(x), packed, sd, bd)
+    y3 = rf.linear(_to_dev(x).view(2, 3, 128), packed, sd, bd)
+    assert y3.shape == (2, 3, 96) and torch.equal(y3.view(6, 96), ref)
+    wide = torch.zeros(6, 256, dtype=torch.float16, device=DEV)
+    wide[:, 64:192] = _to_dev(x)
+    assert torch.equal(rf.linear(wide[:, 64:192], packed, sd, bd), ref)  # strided rows
+    odd = torch.zeros(6 * 128 + 1, dtype=torch.float16, device=DEV)[1:].view(6, 128)
+    odd.copy_(_to_dev(x))  # misaligned base address -> copied internally
+    assert torch.equal(rf.linear(odd, packed, sd, bd), ref)
+    out = torch.empty(6, 96, dtype=torch.float16, device=DEV)
+    rf.linear_into(_to_dev(x), packed, sd, bd, out)
+    assert torch.equal(out, ref)
+    empty = rf.linear(torch.zeros(0, 128, dtype=torch.float16, device=DEV), packed, sd, bd)
+    assert empty.shape == (0, 96)
+
+
+def test_op_errors_on_device():
+    x, q, s, _ = make_case(2, 48, 128, seed=14)
+    packed, sd = rf.pack_weight(_to_dev(q)), _to_dev(s)
+    with pytest.raises(RuntimeError, match="packed weight"):
+        rf.linear(_to_dev(x), _to_dev(q), sd)  # row-major weight, not packed
+    with pytest.raises(RuntimeError, match="GEMV|cannot run"):
+        rf.linear(torch.zeros(65, 128, dtype=torch.float16, device=DEV), packed, sd,
+                  kernel=rf.KERNEL_GEMV)
+    with pytest.raises(RuntimeError, match="bias"):
+        rf.linear(_to_dev(x), packed, sd, torch.zeros(47, dtype=torch.float16, device=DEV))
+
+
+def test_w8a16_linear_module_forward():
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(512, 200, bias=True)
+    mod = rf.W8A16Linear.from_linear(lin).to(DEV)
+    x = o.make_activation(21, 5, 512)
+    y = mod(_to_dev(x)).cpu().numpy()
+    q, s = rf.quantize_linear_per_channel(lin.weight.detach())
+    assert_parity(y, x, q.numpy(), s.numpy(), lin.bias.detach().half().numpy(), label="module")
+
+
+def test_capi_direct_call():
+    """Call rf_w8a16_linear through ctypes, as a non-torch host would."""
+    lib = capi.load()
+    x, q, s, _ = make_case(3, 1024, 4096, seed=15)
+    xd, sd = _to_dev(x), _to_dev(s)
+    packed = rf.pack_weight(_to_dev(q))
+    y = torch.empty(3, 1024, dtype=torch.float16, device=DEV)
+    ws_bytes = lib.rf_w8a16_workspace_bytes(3, 1024, 4096)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    for kern in (capi.KERNEL_GEMV, capi.KERNEL_GEMM):
+        st = lib.rf_w8a16_linear(xd.data_ptr(), 4096, packed.data_ptr(), capi.LAYOUT_TILE16X64,
+                                 sd.data_ptr(), None, y.data_ptr(), 1024, 3, 1024, 4096, kern,
+                                 ws.data_ptr(), ws_bytes, ctypes.c_void_p(stream))
+        capi.check(st, "rf_w8a16_linear")
+        torch.cuda.synchronize()
+        assert_parity(y.cpu().numpy(), x, q, s, None, label=f"ctypes kernel={kern}")
+    assert lib.rf_w8a16_linear(xd.data_ptr(), 4096, packed.data_ptr(), capi.LAYOUT_TILE16X64,
+                               sd.data_ptr(), None, y.data_ptr(), 1024, 3, 1024, 4096,
+                               capi.KERNEL_GEMV, None, 0, ctypes.c_void_p(stream)) in (
+        capi.EWORKSPACE, capi.OK)

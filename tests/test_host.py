@@ -1,0 +1,217 @@
+"""CPU tests of the host side: C-ABI exports, the packer, op schemas, errors.
+
+No compute call reaches a GPU here.  Error paths mirror the reference's
+pre-launch checks (src/ops/rpu_linear.cpp:1119-1134, rpu_linear_gemv.cpp:105-123).
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import rhinoforge_amd as rf
+from rhinoforge_amd import capi
+from oracle import w8a16 as o
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> list[str]:
+    text = (ROOT / "include" / "w8a16.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rf_w8a16_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    assert declared_functions() == sorted(capi.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(capi.LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert capi.load().rf_w8a16_abi_version() == 1
+
+
+def test_status_strings():
+    for st in range(0, 8):
+        assert capi.status_str(st)
+    assert "unknown" in capi.status_str(99)
+
+
+def test_packed_bytes():
+    lib = capi.load()
+    assert lib.rf_w8a16_packed_bytes(3072, 1024) == 3072 * 1024
+    assert lib.rf_w8a16_packed_bytes(151936, 5120) == 151936 * 5120
+    assert lib.rf_w8a16_packed_bytes(17, 72) == 32 * 128
+    assert lib.rf_w8a16_packed_bytes(0, 64) == 0
+    assert lib.rf_w8a16_packed_bytes(16, -1) == 0
+
+
+def _layout_index(n, k, kblocks):
+    """Byte offset of q[n][k] in TILE16X64, from the definition in include/w8a16.h."""
+    nb, nl = divmod(n, 16)
+    kb, kk = divmod(k, 64)
+    lane = nl + 16 * (kk // 16)
+    return (nb * kblocks + kb) * 1024 + lane * 16 + (kk % 16)
+
+
+@pytest.mark.parametrize("n,k", [(16, 64), (17, 72), (100, 8), (48, 320), (1, 1)])
+def test_pack_matches_layout_definition_and_round_trips(n, k):
+    rng = np.random.default_rng(n * 1000 + k)
+    q = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
+    packed = rf.pack_weight(torch.from_numpy(q)).numpy().view(np.uint8).ravel()
+    np_, kp = rf.packed_shape(n, k)
+    assert packed.size == np_ * kp
+    kblocks = kp // 64
+    # every logical element lands where the header says, stored as q XOR 0x80
+    idx = np.array([[_layout_index(i, j, kblocks) for j in range(k)] for i in range(n)])
+    assert (packed[idx] == (q.view(np.uint8) ^ 0x80)).all()
+    # padding holds q = 0
+    mask = np.ones(packed.size, bool)
+    mask[idx.ravel()] = False
+    assert (packed[mask] == 0x80).all()
+    # inverse
+    assert (rf.unpack_weight(torch.from_numpy(packed.view(np.int8).reshape(np_, kp)), n, k).numpy()
+            == q).all()
+
+
+def test_pack_is_a_permutation_on_aligned_shapes():
+    q = np.arange(32 * 128, dtype=np.int64).astype(np.uint8).view(np.int8).reshape(32, 128)
+    p = rf.pack_weight(torch.from_numpy(q)).numpy().view(np.uint8).ravel()
+    assert sorted((p ^ 0x80).tolist()) == sorted(q.view(np.uint8).ravel().tolist())
+
+
+def test_capi_pack_argument_errors():
+    lib = capi.load()
+    q = np.zeros((16, 64), np.int8)
+    dst = np.zeros(16 * 64, np.uint8)
+    qp, dp = q.ctypes.data, dst.ctypes.data
+    assert lib.rf_w8a16_pack_weight(qp, 16, 64, 64, dp, 16 * 64) == capi.OK
+    assert lib.rf_w8a16_pack_weight(qp, 16, 64, 63, dp, 16 * 64) == capi.EINVAL  # ldq < K
+    assert lib.rf_w8a16_pack_weight(qp, 16, 64, 64, dp, 100) == capi.EINVAL      # dst too small
+    assert lib.rf_w8a16_pack_weight(None, 16, 64, 64, dp, 16 * 64) == capi.EINVAL
+    assert lib.rf_w8a16_unpack_weight(dp, 0, 64, qp, 64) == capi.EINVAL
+
+
+def test_capi_linear_validation_without_gpu():
+    """Argument checks run before any device query; nothing is dereferenced."""
+    lib = capi.load()
+    fake = 1 << 20  # 16-byte aligned, never dereferenced before validation fails
+    args = dict(x=fake, ldx=1024, w=fake, layout=capi.LAYOUT_TILE16X64, s=fake, b=None,
+                y=fake, ldy=3072, M=1, N=3072, K=1024, kernel=0, ws=None, wsb=0, stream=None)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.rf_w8a16_linear(a["x"], a["ldx"], a["w"], a["layout"], a["s"], a["b"], a["y"],
+                                   a["ldy"], a["M"], a["N"], a["K"], a["kernel"], a["ws"],
+                                   a["wsb"], a["stream"])
+
+    assert call(x=None) == capi.EINVAL
+    assert call(M=0) == capi.EINVAL
+    assert call(N=0) == capi.EINVAL
+    assert call(ldx=1000) == capi.EINVAL
+    assert call(ldy=3000) == capi.EINVAL
+    assert call(layout=capi.LAYOUT_ROWMAJOR) == capi.ELAYOUT
+    assert call(K=1020, ldx=1024) == capi.EALIGN
+    assert call(x=fake + 2) == capi.EALIGN
+    assert call(ldx=1028) == capi.EALIGN
+    assert call(kernel=7) in (capi.EINVAL, capi.EHIP, capi.EDEVICE)
+    # A valid call on a machine without a gfx950 device never reports success.
+    assert call() in (capi.EHIP, capi.EDEVICE)
+
+
+def test_select_kernel_policy():
+    assert rf.select_kernel(1, 4096, 4096) == rf.KERNEL_GEMV
+    assert rf.select_kernel(16, 151936, 5120) == rf.KERNEL_GEMV
+    assert rf.select_kernel(64, 4096, 4096) == rf.KERNEL_GEMV
+    assert rf.select_kernel(65, 4096, 4096) == rf.KERNEL_GEMM
+    assert rf.select_kernel(2048, 12288, 4096) == rf.KERNEL_GEMM
+    with pytest.raises(RuntimeError):
+        rf.select_kernel(0, 16, 16)
+
+
+def test_workspace_bytes_counter_region():
+    lib = capi.load()
+    for m, n, k in [(1, 1024, 4096), (16, 4096, 12288), (2048, 4096, 4096)]:
+        assert lib.rf_w8a16_workspace_bytes(m, n, k) >= capi.WS_COUNTER_BYTES
+    assert lib.rf_w8a16_workspace_bytes(0, 16, 16) == 0
+
+
+# ---------------------------------------------------------------- torch op
+def test_torch_op_schemas_registered():
+    for name in ("linear", "linear_into", "pack_weight", "unpack_weight", "select_kernel"):
+        assert hasattr(torch.ops.w8a16, name)
+
+
+def test_torch_op_meta_shape():
+    x = torch.empty(2, 3, 1024, dtype=torch.float16, device="meta")
+    w = torch.empty(3072, 1024, dtype=torch.int8, device="meta")
+    s = torch.empty(3072, dtype=torch.float16, device="meta")
+    assert rf.linear(x, w, s).shape == (2, 3, 3072)
+
+
+def _cpu_args(n=48, k=128):
+    q = torch.randint(-127, 128, (n, k), dtype=torch.int8)
+    return (torch.zeros(2, k, dtype=torch.float16), rf.pack_weight(q),
+            torch.ones(n, dtype=torch.float16))
+
+
+def test_torch_op_refuses_cpu_tensors():
+    x, w, s = _cpu_args()
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        rf.linear(x, w, s)
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        rf.linear_into(x, w, s, None, torch.empty(2, 48, dtype=torch.float16))
+
+
+@pytest.mark.parametrize("bad", ["x_dtype", "w_dtype", "s_dtype", "layout"])
+def test_torch_op_argument_errors(bad):
+    x, w, s = _cpu_args()
+    kw = {}
+    if bad == "x_dtype":
+        x = x.float()
+    elif bad == "w_dtype":
+        w = w.to(torch.uint8)
+    elif bad == "s_dtype":
+        s = s.float()
+    else:
+        kw["layout"] = rf.LAYOUT_ROWMAJOR
+    with pytest.raises(RuntimeError):
+        torch.ops.w8a16.linear(x, w, s, None, kw.get("layout", 1), 0)
+
+
+def test_pack_weight_rejects_bad_input():
+    with pytest.raises(RuntimeError):
+        rf.pack_weight(torch.zeros(4, 4, dtype=torch.float16))
+    with pytest.raises(RuntimeError):
+        rf.pack_weight(torch.zeros(4, dtype=torch.int8))
+    with pytest.raises(RuntimeError):
+        rf.unpack_weight(torch.zeros(10, dtype=torch.int8), 16, 64)
+
+
+# ---------------------------------------------------------------- quant (torch)
+@pytest.mark.parametrize("seed", [0, 1])
+def test_package_quantizer_bit_exact_vs_oracle(seed):
+    w = o.make_weight(seed, 130, 300)
+    w[5] = 0
+    q, s = rf.quantize_linear_per_channel(torch.from_numpy(w))
+    q2, s2 = o.quantize_linear_per_channel(w)
+    assert q.dtype == torch.int8 and s.dtype == torch.float16
+    assert (q.numpy() == q2).all() and (s.numpy().view(np.uint16) == s2.view(np.uint16)).all()
+    d = rf.dequantize_linear_per_channel(q, s).numpy()
+    assert (d.view(np.uint16) == o.dequantize_linear_per_channel(q2, s2).view(np.uint16)).all()
+
+
+def test_w8a16_linear_module_construction_on_cpu():
+    lin = torch.nn.Linear(128, 40, bias=True)
+    mod = rf.W8A16Linear.from_linear(lin)
+    assert mod.weight.shape == rf.packed_shape(40, 128)
+    q, s = rf.quantize_linear_per_channel(lin.weight.detach())
+    assert torch.equal(mod.rowmajor_weight(), q) and torch.equal(mod.weight_scale, s)
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        mod(torch.zeros(1, 128, dtype=torch.float16))
