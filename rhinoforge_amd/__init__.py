@@ -8,7 +8,7 @@ HIP kernels behind a C ABI (``include/w8a16.h``) and a thin torch-library op
 Importing the package loads ``lib/librf_w8a16_torch.so`` (which links
 ``lib/librf_w8a16.so``).  If the libraries are missing the import fails
 loudly: there is no CPU or pure-PyTorch fallback for the compute path.
-Build them with ``python -m rhinoforge_amd._build``.
+Build them with ``python rhinoforge_amd/_build.py``.
 """
 from __future__ import annotations
 
@@ -24,7 +24,7 @@ if not TORCH_OP_LIBRARY.is_file() or not CAPI_LIBRARY.is_file():
     raise ImportError(
         f"rhinoforge_amd native libraries not built ({TORCH_OP_LIBRARY.name}, "
         f"{CAPI_LIBRARY.name} missing under {_LIBDIR}); run "
-        "`python -m rhinoforge_amd._build` (or __graft_entry__.build())"
+        "`python rhinoforge_amd/_build.py` (or __graft_entry__.build())"
     )
 torch.ops.load_library(str(TORCH_OP_LIBRARY))
 

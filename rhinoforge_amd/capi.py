@@ -55,7 +55,7 @@ def load() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not LIB_PATH.is_file():
-            raise OSError(f"{LIB_PATH} not built; run `python -m rhinoforge_amd._build`")
+            raise OSError(f"{LIB_PATH} not built; run `python rhinoforge_amd/_build.py`")
         lib = ctypes.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

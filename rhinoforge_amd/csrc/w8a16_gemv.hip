@@ -1,20 +1,33 @@
 // Decode GEMV / skinny GEMM for W8A16, M <= 64 (gfx950).
 //
 // HBM-bound: every call streams N*K weight bytes once.  Design:
-//   * one workgroup = 4 wavefronts = `NS` strips of 16 output channels over
+//   * a workgroup of W wavefronts owns NS strips of 16 output channels over
 //     one K split; the wavefronts interleave the split's 1 KB weight tiles
-//     (wave w takes tiles w, w+4, ...), so each wavefront-wide load is one
-//     fully coalesced 1 KB tile and a workgroup step reads 4 KB contiguous;
+//     (wave w takes tiles w, w+W, ...), so each wavefront-wide load is one
+//     fully coalesced 1 KB tile and a workgroup step reads W KB contiguous
+//     per strip;
 //   * weights are dequantized in registers (v_perm + v_pk_add, exact) and
 //     fed to v_mfma_f32_16x16x32_f16 with the activation rows as the A
 //     operand, so the K reduction inside a tile happens in the matrix core;
-//   * loads are software-pipelined: the next stage of U tiles per wavefront
-//     is in flight while the current one is converted and multiplied;
-//   * the four wavefronts' fp32 partials are summed through LDS; with K
-//     split across workgroups, partials go to the workspace and the last
-//     workgroup to arrive (device-scope counter) adds them in split order
-//     (deterministic), applies scale and bias, stores fp16, and re-zeroes
-//     the counter.
+//     the activation fragment of a tile is reused for all NS strips;
+//   * weight loads are software-pipelined two stages deep: the next U tiles
+//     per wavefront are in flight while the current U are converted and
+//     multiplied;
+//   * activations come either straight from global memory (L2-resident,
+//     prefetched with the weights) or, when XL is set, from a copy of the
+//     split's x[0:M, Krange] that the workgroup stages in LDS once;
+//   * the wavefronts' fp32 partials are summed through LDS in a fixed order;
+//     with K split across workgroups the partials go to the workspace and
+//     the last workgroup to arrive sums them in split order (deterministic),
+//     applies scale and bias, stores fp16 and re-zeroes its counter.
+//
+// Split-K hand-off without L2 flushes: on gfx950 each XCD has its own L2,
+// and a device-scope fence (__threadfence) writes back and invalidates the
+// whole L2 of the issuing XCD.  Instead the partials are written and read
+// with relaxed device-scope atomic stores/loads (global_store/load ... sc1,
+// coherent at device scope by themselves), and each workgroup waits for its
+// stores to complete (s_waitcnt vmcnt(0)) before it bumps the counter.
+//
 // The per-channel scale is applied once in the epilogue: s[n] factors out
 // of the K sum, y[m,n] = s[n] * sum_k x[m,k] q[n,k] (+ b[n]).
 #include "w8a16_common.h"
@@ -24,8 +37,8 @@
 namespace rf {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * kWave;
+constexpr int kMaxSplits = 16;
+constexpr int kMaxGroupsSplit = RF_W8A16_WS_COUNTER_BYTES / 4;
 
 struct GemvKernelArgs {
   const _Float16* x;
@@ -45,11 +58,20 @@ struct GemvKernelArgs {
   uint32_t* counters;  // [groups]
 };
 
-// Activation fragment of one tile for m-tile `mt`: x[m][k .. k+15] with
-// m = 16*mt + lane%16 and k = 64*kb + 16*(lane/16); zero outside [M) x [K).
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Activation fragment of one tile for m-tile `mt` read from global memory:
+// x[m][k .. k+15] with m = 16*mt + lane%16, k = 64*kb + 16*(lane/16); rows
+// m >= M are zero.  K % 8 == 0, so a chunk that starts below K ends below K.
 template <int MT>
-__device__ __forceinline__ void load_x(const GemvKernelArgs& a, int kb, int lane,
-                                       half8 (&xa)[MT][2]) {
+__device__ __forceinline__ void load_x_global(const GemvKernelArgs& a, int kb, int lane,
+                                              half8 (&xa)[MT][2]) {
   const int k = kb * kTileK + 16 * (lane >> 4);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -65,15 +87,62 @@ __device__ __forceinline__ void load_x(const GemvKernelArgs& a, int kb, int lane
   }
 }
 
-template <int MT, int NS, int U>
-__global__ __launch_bounds__(kThreads) void w8a16_gemv_kernel(GemvKernelArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+// The same fragment read from the LDS copy of x (row pitch `pitch` bytes,
+// column 0 = first K position of the split; rows >= M are never read).
+template <int MT>
+__device__ __forceinline__ void load_x_lds(const uint8_t* xs, int pitch, int M, int kl, int lane,
+                                           half8 (&xa)[MT][2]) {
+  const int k = kl * kTileK + 16 * (lane >> 4);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + (lane & 15);
+    uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
+    if (m < M) {
+      const uint8_t* p = xs + m * pitch + k * 2;
+      v0 = *reinterpret_cast<const uint4*>(p);
+      v1 = *reinterpret_cast<const uint4*>(p + 16);
+    }
+    xa[mt][0] = as_half8(v0);
+    xa[mt][1] = as_half8(v1);
+  }
+}
+
+// Dynamic LDS bytes the kernel needs: max(x copy, cross-wave reduction).
+inline size_t gemv_lds_bytes(int MT, int NS, int W, bool XL, int M, int kb_per_split) {
+  const size_t red = (size_t)W * MT * NS * kWave * sizeof(floatx4);
+  const size_t xb = XL ? (size_t)M * (size_t)(kb_per_split * kTileK * 2 + 16) : 0;
+  return red > xb ? red : xb;
+}
+
+template <int MT, int NS, int W, int U, bool XL, bool NT>
+__global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int kThreads = W * kWave;
+  constexpr int T = MT * NS;  // 16x16 output tiles per workgroup
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int group = blockIdx.x;
   const int split = blockIdx.y;
   const int strip0 = group * NS;
   const int kb0 = split * a.kb_per_split;
   const int kb1 = min(kb0 + a.kb_per_split, a.kblocks);
+  const int ntiles = kb1 - kb0;
+
+  // ---- stage x[0:M, split's K range] in LDS -----------------------------
+  int pitch = 0;
+  if (XL) {
+    pitch = ntiles * kTileK * 2 + 16;  // +16 B: rows start on different banks
+    const int row_chunks = ntiles * (kTileK / 8);
+    const int total = a.M * row_chunks;
+    for (int c = tid; c < total; c += kThreads) {
+      const int m = c / row_chunks, cc = c - m * row_chunks;
+      const int k = kb0 * kTileK + cc * 8;
+      const uint4 v = k < a.K ? load_u4(a.x + (int64_t)m * a.ldx + k) : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(smem + m * pitch + cc * 16) = v;
+    }
+    __syncthreads();
+  }
 
   floatx4 acc[MT][NS];
 #pragma unroll
@@ -87,149 +156,154 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemv_kernel(GemvKernelArgs a) 
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     strip_ok[s] = (strip0 + s) < a.nstrips;
-    wbase[s] = a.w + ((int64_t)(strip0 + s) * a.kblocks) * kTileBytes + lane * 16;
+    wbase[s] = a.w + ((int64_t)(strip0 + s) * a.kblocks + kb0) * kTileBytes + lane * 16;
   }
 
-  // Stage buffers: U tiles per wavefront per stage.
-  uint4 wcur[U][NS], wnxt[U][NS];
-  half8 xcur[U][MT][2], xnxt[U][MT][2];
+  // Tiles of this wavefront: local index kl = wave + W*i, i in [0, my).
+  const int my = ntiles > wave ? (ntiles - wave + W - 1) / W : 0;
+  const int stages = (my + U - 1) / U;
 
-  auto load_stage = [&](int it, uint4 (&wv)[U][NS], half8 (&xv)[U][MT][2]) {
+  uint4 wA[U][NS], wB[U][NS];
+  half8 xA[XL ? 1 : U][MT][2], xB[XL ? 1 : U][MT][2];
+
+  auto load_stage = [&](int st, uint4 (&wv)[U][NS], half8 (&xv)[XL ? 1 : U][MT][2]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int kb = kb0 + wave + kWaves * (it * U + u);
-      const bool ok = kb < kb1;
+      const int kl = wave + W * (st * U + u);
+      const bool ok = kl < ntiles;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        wv[u][s] = (ok && strip_ok[s]) ? load_u4_stream(wbase[s] + (int64_t)kb * kTileBytes)
-                                       : make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+        if (ok && strip_ok[s]) {
+          const uint8_t* p = wbase[s] + (int64_t)kl * kTileBytes;
+          wv[u][s] = NT ? load_u4_stream(p) : load_u4(p);
+        } else {
+          wv[u][s] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+        }
       }
-      if (ok) {
-        load_x<MT>(a, kb, lane, xv[u]);
-      } else {
+      if (!XL) {
+        if (ok) {
+          load_x_global<MT>(a, kb0 + kl, lane, xv[XL ? 0 : u]);
+        } else {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) xv[u][mt][0] = xv[u][mt][1] = half8{};
+          for (int mt = 0; mt < MT; ++mt) xv[XL ? 0 : u][mt][0] = xv[XL ? 0 : u][mt][1] = half8{};
+        }
       }
     }
   };
 
-  const int my_tiles = (kb1 - kb0 - wave + kWaves - 1) / kWaves;  // tiles for this wave
-  const int stages = (my_tiles + U - 1) / U;
-
-  if (stages > 0) load_stage(0, wcur, xcur);
-  for (int it = 0; it < stages; ++it) {
-    if (it + 1 < stages) load_stage(it + 1, wnxt, xnxt);
+  auto compute_stage = [&](int st, const uint4 (&wv)[U][NS], half8 (&xv)[XL ? 1 : U][MT][2]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const int kl = wave + W * (st * U + u);
+      if (kl >= ntiles) break;  // uniform across the wavefront
+      half8 xl[MT][2];
+      if (XL) load_x_lds<MT>(smem, pitch, a.M, kl, lane, xl);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const half8 b0 = dequant8(wcur[u][s].x, wcur[u][s].y);
-        const half8 b1 = dequant8(wcur[u][s].z, wcur[u][s].w);
+        const half8 b0 = dequant8(wv[u][s].x, wv[u][s].y);
+        const half8 b1 = dequant8(wv[u][s].z, wv[u][s].w);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[mt][s] = mfma16x16x32(xcur[u][mt][0], b0, acc[mt][s]);
-          acc[mt][s] = mfma16x16x32(xcur[u][mt][1], b1, acc[mt][s]);
+          const half8 x0 = XL ? xl[mt][0] : xv[XL ? 0 : u][mt][0];
+          const half8 x1 = XL ? xl[mt][1] : xv[XL ? 0 : u][mt][1];
+          acc[mt][s] = mfma16x16x32(x0, b0, acc[mt][s]);
+          acc[mt][s] = mfma16x16x32(x1, b1, acc[mt][s]);
         }
       }
     }
-    if (it + 1 < stages) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) wcur[u][s] = wnxt[u][s];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          xcur[u][mt][0] = xnxt[u][mt][0];
-          xcur[u][mt][1] = xnxt[u][mt][1];
-        }
-      }
-    }
+  };
+
+  // Two-stage pipeline, unrolled by two so the buffers never move.
+  if (stages > 0) load_stage(0, wA, xA);
+  for (int st = 0; st < stages; st += 2) {
+    if (st + 1 < stages) load_stage(st + 1, wB, xB);
+    compute_stage(st, wA, xA);
+    if (st + 1 >= stages) break;
+    if (st + 2 < stages) load_stage(st + 2, wA, xA);
+    compute_stage(st + 1, wB, xB);
   }
 
-  // ---- cross-wavefront reduction through LDS --------------------------
-  __shared__ floatx4 red[kWaves][MT * NS][kWave];
+  // ---- cross-wavefront reduction through LDS (fixed order) --------------
+  if (XL) __syncthreads();  // everyone is done with the x copy
+  float* red = reinterpret_cast<float*>(smem);  // [W][T][64 lanes][4]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int s = 0; s < NS; ++s) red[wave][mt * NS + s][lane] = acc[mt][s];
+    for (int s = 0; s < NS; ++s)
+      *reinterpret_cast<floatx4*>(&red[((wave * T + mt * NS + s) * kWave + lane) * 4]) = acc[mt][s];
   __syncthreads();
 
-  // Tile t = mt*NS + s is finished by wavefront t % 4.
-  const int n_in_strip = lane & 15;
-  const int m_sub = 4 * (lane >> 4);
-  for (int t = wave; t < MT * NS; t += kWaves) {
-    const int mt = t / NS, s = t % NS;
-    floatx4 sum = red[0][t][lane];
+  // Element e = (tile t, lane ln, row r) of the workgroup's T tiles; lane ln
+  // of an MFMA result holds D[4*(ln/16) + r][ln%16].
+  for (int e = tid; e < T * 256; e += kThreads) {
+    const int t = e >> 8, j = e & 255, ln = j >> 2, r = j & 3;
+    float sum = red[t * 256 + j];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) sum += red[w][t][lane];
-    const int n = (strip0 + s) * 16 + n_in_strip;
+    for (int w = 1; w < W; ++w) sum += red[(w * T + t) * 256 + j];
+    const int mt = t / NS, s = t % NS;
+    const int n = (strip0 + s) * 16 + (ln & 15);
+    const int m = mt * 16 + 4 * (ln >> 4) + r;
+    if (m >= a.M || strip0 + s >= a.nstrips) continue;
     if (a.splits == 1) {
       if (n < a.N) {
         const float sc = (float)a.scale[n];
         const float bi = a.bias ? (float)a.bias[n] : 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = mt * 16 + m_sub + r;
-          if (m < a.M) a.y[(int64_t)m * a.ldy + n] = (_Float16)__builtin_fmaf(sum[r], sc, bi);
-        }
+        a.y[(int64_t)m * a.ldy + n] = (_Float16)__builtin_fmaf(sum, sc, bi);
       }
-    } else if (strip0 + s < a.nstrips) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = mt * 16 + m_sub + r;
-        if (m < a.M) a.partial[((int64_t)split * a.M + m) * a.np + n] = sum[r];
-      }
+    } else {
+      store_coherent(&a.partial[((int64_t)split * a.M + m) * a.np + n], sum);
     }
   }
   if (a.splits == 1) return;
 
-  // ---- split-K: last workgroup to arrive reduces in split order ---------
+  // ---- split-K: the last workgroup to arrive reduces in split order ------
   __shared__ uint32_t is_last;
-  __threadfence();  // release this workgroup's partials (device scope)
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(&a.counters[group], 1u);
+  if (tid == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(&a.counters[group], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = (prev == (uint32_t)(a.splits - 1)) ? 1u : 0u;
   }
   __syncthreads();
   if (!is_last) return;
-  __threadfence();  // acquire the other workgroups' partials
 
-  // Each thread finishes (m, n) outputs of this group, coalesced along n.
   const int nrows = min(NS, a.nstrips - strip0) * 16;
   const int total = a.M * nrows;
-  for (int i = threadIdx.x; i < total; i += kThreads) {
+  for (int i = tid; i < total; i += kThreads) {
     const int m = i / nrows;
-    const int n = strip0 * 16 + (i % nrows);
-    float sum = 0.f;
-    for (int sp = 0; sp < a.splits; ++sp)
-      sum += __builtin_nontemporal_load(&a.partial[((int64_t)sp * a.M + m) * a.np + n]);
+    const int n = strip0 * 16 + (i - m * nrows);
+    // Issue every split's load before summing (one memory round trip), then
+    // add in split order.
+    float part[kMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+      part[sp] = sp < a.splits ? load_coherent(&a.partial[((int64_t)sp * a.M + m) * a.np + n]) : 0.f;
+    float sum = part[0];
+#pragma unroll
+    for (int sp = 1; sp < kMaxSplits; ++sp)
+      if (sp < a.splits) sum += part[sp];
     if (n < a.N) {
       const float sc = (float)a.scale[n];
       const float bi = a.bias ? (float)a.bias[n] : 0.f;
       a.y[(int64_t)m * a.ldy + n] = (_Float16)__builtin_fmaf(sum, sc, bi);
     }
   }
-  if (threadIdx.x == 0) atomicExch(&a.counters[group], 0u);  // leave the counter zeroed
+  if (tid == 0)
+    __hip_atomic_store(&a.counters[group], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int MT, int NS, int U>
+template <int MT, int NS, int W, int U, bool XL, bool NT>
 hipError_t launch_t(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t stream) {
+  const size_t lds = gemv_lds_bytes(MT, NS, W, XL, ka.M, ka.kb_per_split);
+  if (lds > 65536) return hipErrorInvalidValue;
   dim3 grid(p.groups, p.splits, 1);
-  hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, U>), grid, dim3(kThreads), 0, stream, ka);
+  hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, W, U, XL, NT>), grid, dim3(W * kWave), lds, stream,
+                     ka);
   return hipGetLastError();
 }
 
-}  // namespace
-
-size_t gemv_workspace_bytes(const GemvPlan& p, int M, int N) {
-  if (p.splits <= 1) return 0;
-  const int64_t np = round_up(N, 16);
-  return (size_t)p.splits * (size_t)M * (size_t)np * sizeof(float);
-}
-
-hipError_t launch_gemv(const LinearArgs& a, const GemvPlan& p, void* workspace,
-                       hipStream_t stream) {
+GemvKernelArgs make_args(const LinearArgs& a, const GemvPlan& p, void* workspace) {
   GemvKernelArgs ka;
   ka.x = a.x;
   ka.ldx = a.ldx;
@@ -248,37 +322,142 @@ hipError_t launch_gemv(const LinearArgs& a, const GemvPlan& p, void* workspace,
   ka.np = a.nstrips * 16;
   // Workspace: [counters | partials]; counter region size fixed by the ABI.
   ka.counters = reinterpret_cast<uint32_t*>(workspace);
-  ka.partial = workspace ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + RF_W8A16_WS_COUNTER_BYTES)
+  ka.partial = workspace ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
+                                                    RF_W8A16_WS_COUNTER_BYTES)
                          : nullptr;
+  return ka;
+}
 
-  switch (p.mt * 100 + p.ns) {
-    case 101: return launch_t<1, 1, 4>(ka, p, stream);
-    case 102: return launch_t<1, 2, 4>(ka, p, stream);
-    case 104: return launch_t<1, 4, 2>(ka, p, stream);
-    case 201: return launch_t<2, 1, 2>(ka, p, stream);
-    case 202: return launch_t<2, 2, 2>(ka, p, stream);
-    case 401: return launch_t<4, 1, 2>(ka, p, stream);
-    case 402: return launch_t<4, 2, 1>(ka, p, stream);
+// Kernel configurations the planner chooses from (all stream weights with
+// non-temporal loads).  Measured on MI355X over the BASELINE decode shapes.
+enum GemvCfgId {
+  kG1x1W16U4,   // MT=1 NS=1 W=16 U=4
+  kG1x1W16U2,   // MT=1 NS=1 W=16 U=2   (long K)
+  kG1x1W8U4XL,  // MT=1 NS=1 W=8  U=4, x staged in LDS (many strips)
+  kG1x1W4U4,    // MT=1 NS=1 W=4  U=4
+  kG1x2W16U2,   // MT=1 NS=2 W=16 U=2
+  kG1x4W8U2,    // MT=1 NS=4 W=8  U=2   (M 5..16: x fragment reused 4x)
+  kG1x4W4U2,    // MT=1 NS=4 W=4  U=2
+  kG2x4W4U2,    // MT=2 NS=4 W=4  U=2
+  kG2x2W8U1,    // MT=2 NS=2 W=8  U=1
+  kG2x1W8U4,    // MT=2 NS=1 W=8  U=4
+  kG4x2W8U1,    // MT=4 NS=2 W=8  U=1
+  kG4x2W4U1,    // MT=4 NS=2 W=4  U=1
+  kGemvCfgCount
+};
+
+struct GemvCfgDesc {
+  int mt, ns, w;
+  bool xl;
+};
+
+constexpr GemvCfgDesc kGemvCfgs[kGemvCfgCount] = {
+    {1, 1, 16, false}, {1, 1, 16, false}, {1, 1, 8, true}, {1, 1, 4, false},
+    {1, 2, 16, false}, {1, 4, 8, false},  {1, 4, 4, false}, {2, 4, 4, false},
+    {2, 2, 8, false},  {2, 1, 8, false},  {4, 2, 8, false}, {4, 2, 4, false},
+};
+
+bool lds_fits(int cfg, int M, int kb_per_split) {
+  const GemvCfgDesc& d = kGemvCfgs[cfg];
+  return gemv_lds_bytes(d.mt, d.ns, d.w, d.xl, M, kb_per_split) <= 65536;
+}
+
+}  // namespace
+
+size_t gemv_workspace_bytes(const GemvPlan& p, int M, int N) {
+  if (p.splits <= 1) return 0;
+  const int64_t np = round_up(N, 16);
+  return (size_t)p.splits * (size_t)M * (size_t)np * sizeof(float);
+}
+
+hipError_t launch_gemv(const LinearArgs& a, const GemvPlan& p, void* workspace,
+                       hipStream_t stream) {
+  const GemvKernelArgs ka = make_args(a, p, workspace);
+  switch (p.cfg) {
+    case kG1x1W16U4: return launch_t<1, 1, 16, 4, false, true>(ka, p, stream);
+    case kG1x1W16U2: return launch_t<1, 1, 16, 2, false, true>(ka, p, stream);
+    case kG1x1W8U4XL: return launch_t<1, 1, 8, 4, true, true>(ka, p, stream);
+    case kG1x1W4U4: return launch_t<1, 1, 4, 4, false, true>(ka, p, stream);
+    case kG1x2W16U2: return launch_t<1, 2, 16, 2, false, true>(ka, p, stream);
+    case kG1x4W8U2: return launch_t<1, 4, 8, 2, false, true>(ka, p, stream);
+    case kG1x4W4U2: return launch_t<1, 4, 4, 2, false, true>(ka, p, stream);
+    case kG2x4W4U2: return launch_t<2, 4, 4, 2, false, true>(ka, p, stream);
+    case kG2x2W8U1: return launch_t<2, 2, 8, 1, false, true>(ka, p, stream);
+    case kG2x1W8U4: return launch_t<2, 1, 8, 4, false, true>(ka, p, stream);
+    case kG4x2W8U1: return launch_t<4, 2, 8, 1, false, true>(ka, p, stream);
+    case kG4x2W4U1: return launch_t<4, 2, 4, 1, false, true>(ka, p, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
+// Kernel choice per shape: the analogue of the reference's W8A16 tile
+// tables (src/ops/rpu_linear_tiling.h:69-127, selectors :544-595), but as
+// rules over (M, strips of 16 channels, 64-wide K blocks), tuned on MI355X:
+//   * M <= 4: the activation fragment is nearly free, so one strip per
+//     workgroup and as many wavefronts as keep ~16 per CU busy;
+//   * M 5..16: the fragment costs twice the weight bytes per tile, so four
+//     strips share it when there are enough strips to fill the chip;
+//   * M 17..64: two / four 16-row m-tiles per wavefront;
+//   * K splits only where the strips alone cannot fill 256 CUs.
 GemvPlan plan_gemv(int M, int N, int K, const DeviceInfo& dev) {
-  GemvPlan p;
   const int nstrips = (int)ceil_div(N, 16);
   const int kblocks = (int)ceil_div(K, 64);
-  p.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  p.ns = 1;
+  // Thresholds are in strips for a 256-CU part; scale for smaller parts.
+  const int cu = dev.cus > 0 ? dev.cus : 256;
+  auto strips_ge = [&](int n256) { return (int64_t)nstrips * 256 >= (int64_t)n256 * cu; };
+  int cfg, splits = 1;
+  if (M <= 4) {
+    if (strips_ge(640)) {
+      cfg = kG1x1W8U4XL;
+      if (!lds_fits(cfg, M, kblocks)) cfg = kG1x1W4U4;
+    } else if (strips_ge(257)) {
+      cfg = kG1x2W16U2;
+    } else if (kblocks >= 128) {
+      cfg = kG1x1W16U2;
+    } else {
+      cfg = kG1x1W16U4;
+    }
+  } else if (M <= 16) {
+    if (strips_ge(2048)) {
+      cfg = kG1x4W4U2;
+    } else if (strips_ge(512)) {
+      cfg = kG1x4W8U2;
+    } else if (kblocks >= 128) {
+      cfg = kG1x4W8U2;
+      splits = 4;
+    } else if (!strips_ge(65)) {
+      cfg = kG1x2W16U2;
+      splits = 4;
+    } else {
+      cfg = kG1x1W16U4;
+    }
+  } else if (M <= 32) {
+    if (strips_ge(1024)) {
+      cfg = kG2x4W4U2;
+    } else if (kblocks >= 128) {
+      cfg = kG2x4W4U2;
+      splits = 4;
+    } else if (!strips_ge(65)) {
+      cfg = kG2x1W8U4;
+      splits = 4;
+    } else {
+      cfg = kG2x2W8U1;
+    }
+  } else {
+    if (strips_ge(512)) {
+      cfg = kG4x2W4U1;
+    } else {
+      cfg = kG4x2W8U1;
+      splits = 2;
+    }
+  }
+  GemvPlan p;
+  p.cfg = cfg;
+  p.mt = kGemvCfgs[cfg].mt;
+  p.ns = kGemvCfgs[cfg].ns;
   p.groups = (int)ceil_div(nstrips, p.ns);
-  // Enough workgroups to cover every CU twice; each wavefront keeps >= 2
-  // tiles per split so the pipeline has something to overlap.
-  const int target = 2 * dev.cus;
-  int splits = (int)ceil_div(target, p.groups);
-  const int max_splits = kblocks / (2 * kWaves);
-  if (splits > max_splits) splits = max_splits;
-  if (splits > 16) splits = 16;
-  if (splits < 1) splits = 1;
-  if (p.groups > 16384) splits = 1;  // counter region holds 16384 counters
+  if (p.groups > kMaxGroupsSplit) splits = 1;  // counter region holds kMaxGroupsSplit counters
+  if (splits > kblocks) splits = kblocks;
   p.kb_per_split = (int)ceil_div(kblocks, splits);
   p.splits = (int)ceil_div(kblocks, p.kb_per_split);  // drop empty splits
   return p;

@@ -26,6 +26,7 @@ struct LinearArgs {
 
 // Decode GEMV / skinny-GEMM launch plan (M <= 64).
 struct GemvPlan {
+  int cfg;       // kernel configuration id (w8a16_gemv.hip)
   int mt;        // 16-row m tiles per wavefront (1, 2 or 4)
   int ns;        // 16-channel strips per workgroup
   int splits;    // K splits across workgroups (1 = no workspace use)

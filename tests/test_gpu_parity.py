@@ -244,6 +244,40 @@ def test_edge_shapes(m, n, k, bias):
                       label=f"edge {m}x{n}x{k} {kern}")
 
 
+# One shape per rule of the GEMV planner (w8a16_gemv.hip plan_gemv), so every
+# kernel configuration it can pick runs at least once.
+GEMV_POLICY = [
+    (2, 10240, 512),   # M<=4, >=640 strips: x staged in LDS
+    (4, 10240, 8256),  # same rule, x does not fit in LDS: plain 4-wave config
+    (1, 5000, 320),    # M<=4, 257..639 strips: two strips per workgroup
+    (3, 512, 8192),    # M<=4, long K
+    (1, 512, 1024),    # M<=4, default
+    (8, 32768, 128),   # M 5..16, >=2048 strips
+    (12, 8192, 256),   # M 5..16, >=512 strips
+    (16, 1024, 8192),  # M 5..16, long K: 4-way K split
+    (9, 1000, 1024),   # M 5..16, <=64 strips: 4-way K split
+    (16, 2048, 1024),  # M 5..16, default
+    (20, 16384, 128),  # M 17..32, >=1024 strips
+    (32, 640, 8192),   # M 17..32, long K: 4-way K split
+    (17, 1024, 512),   # M 17..32, <=64 strips: 4-way K split
+    (24, 2048, 512),   # M 17..32, default
+    (40, 8192, 256),   # M 33..64, >=512 strips
+    (64, 1000, 640),   # M 33..64, default: 2-way K split
+]
+
+
+@pytest.mark.parametrize("m,n,k", GEMV_POLICY)
+def test_gemv_every_planner_rule(m, n, k):
+    _say(f"gemv policy M={m} N={n} K={k}")
+    x, q, s, b = make_case(m, n, k, seed=16, bias=True)
+    assert rf.select_kernel(m, n, k) == rf.KERNEL_GEMV
+    packed = rf.pack_weight(_to_dev(q))
+    y1 = run_gpu(x, q, s, b, packed=packed)
+    assert_parity(y1, x, q, s, b, label=f"gemv policy {m}x{n}x{k}")
+    y2 = run_gpu(x, q, s, b, packed=packed)  # split-K counters were left zeroed
+    assert (y1.view(np.uint16) == y2.view(np.uint16)).all()
+
+
 def test_zero_rows_and_extreme_scales():
     n, k = 64, 256
     rng = np.random.default_rng(5)
@@ -308,15 +342,17 @@ def test_input_views_3d_empty_and_linear_into():
 
 
 def test_op_errors_on_device():
-    x, q, s, _ = make_case(2, 48, 128, seed=14)
+    # N=40, K=120: the row-major weight [40, 120] differs in shape from the
+    # packed one [48, 128], so passing it unpacked must be refused.
+    x, q, s, _ = make_case(2, 40, 120, seed=14)
     packed, sd = rf.pack_weight(_to_dev(q)), _to_dev(s)
     with pytest.raises(RuntimeError, match="packed weight"):
         rf.linear(_to_dev(x), _to_dev(q), sd)  # row-major weight, not packed
     with pytest.raises(RuntimeError, match="GEMV|cannot run"):
-        rf.linear(torch.zeros(65, 128, dtype=torch.float16, device=DEV), packed, sd,
+        rf.linear(torch.zeros(65, 120, dtype=torch.float16, device=DEV), packed, sd,
                   kernel=rf.KERNEL_GEMV)
     with pytest.raises(RuntimeError, match="bias"):
-        rf.linear(_to_dev(x), packed, sd, torch.zeros(47, dtype=torch.float16, device=DEV))
+        rf.linear(_to_dev(x), packed, sd, torch.zeros(39, dtype=torch.float16, device=DEV))
 
 
 def test_w8a16_linear_module_forward():
