@@ -9,8 +9,8 @@
 // 16-byte activation-row alignment of a 128-bit load.
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
-#include <vector>
 
 #include "../../include/w8a16.h"
 #include "w8a16_common.h"
@@ -22,24 +22,24 @@ namespace rf {
 // Device properties, cached per device (read-only after the first query).
 // ---------------------------------------------------------------------------
 int device_info(DeviceInfo* out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> state[kMaxDevices];  // 0 = unknown, 1 = cached
+  static DeviceInfo cache[kMaxDevices];
   static std::mutex mu;
-  static std::vector<int> state;  // 0 = unknown, 1 = cached
-  static std::vector<DeviceInfo> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return RF_W8A16_EHIP;
-  std::lock_guard<std::mutex> g(mu);
-  if ((int)state.size() <= dev) {
-    state.resize(dev + 1, 0);
-    cache.resize(dev + 1);
-  }
-  if (!state[dev]) {
-    hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return RF_W8A16_EHIP;
-    DeviceInfo d;
-    d.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-    d.gfx950 = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-    cache[dev] = d;
-    state[dev] = 1;
+  if (dev < 0 || dev >= kMaxDevices) return RF_W8A16_EDEVICE;
+  if (state[dev].load(std::memory_order_acquire) == 0) {
+    std::lock_guard<std::mutex> g(mu);
+    if (state[dev].load(std::memory_order_relaxed) == 0) {
+      hipDeviceProp_t prop;
+      if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return RF_W8A16_EHIP;
+      DeviceInfo d;
+      d.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+      d.gfx950 = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+      cache[dev] = d;
+      state[dev].store(1, std::memory_order_release);
+    }
   }
   *out = cache[dev];
   return RF_W8A16_OK;

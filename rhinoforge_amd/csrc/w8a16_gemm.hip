@@ -1,16 +1,23 @@
 // Prefill GEMM for W8A16 (gfx950): LDS-staged INT8 weight tiles dequantized
 // into fp16 MFMA operands, fp32 accumulation.
 //
-// Workgroup tile BM x BN x 64 (K), 256 threads = 2 x 2 wavefronts, each
-// wavefront owns a (BM/2) x (BN/2) block of 16x16 MFMA accumulators.
-//   * A (activations, fp16) is staged row-major in LDS with a 144-byte row
-//     pitch, so the 16 rows read by one 16-lane group land on distinct banks;
-//   * B (weights) is staged in LDS still as INT8 (half the LDS bytes and
-//     half the global->LDS traffic of an fp16 tile): the TILE16X64 tiles are
-//     copied verbatim, and each lane's 16 bytes are exactly its two MFMA B
-//     operands, dequantized in registers right before the MFMAs;
-//   * double-buffered: the next K step's global loads are issued before the
-//     current step's MFMAs and written to the other LDS buffer afterwards;
+// Workgroup tile BM x BN, WAVES_M x WAVES_N wavefronts, each owning a
+// (BM/WAVES_M) x (BN/WAVES_N) block of 16x16 v_mfma_f32_16x16x32_f16
+// accumulators.
+//   * operands move global -> LDS with global_load_lds_dwordx4 (no VGPR
+//     staging), STAGES ring buffers of KS 64-wide K blocks each, so up to
+//     STAGES-1 K steps are in flight while one is multiplied;
+//   * A (activations, fp16) rows are 128 bytes per K block, chunk-swizzled
+//     (slot p of row r holds chunk p ^ ((r>>1)&7)) so the 16 rows one 16-lane
+//     group reads land on 64 distinct banks;
+//   * B (weights) stays INT8 in LDS (half the LDS bytes and half the
+//     global->LDS traffic of an fp16 tile): TILE16X64 tiles are copied
+//     verbatim and each lane's 16 bytes are exactly its two MFMA B operands,
+//     dequantized in registers right before the MFMAs (exact, v_perm +
+//     v_pk_add);
+//   * tiles are ordered so that the workgroups one XCD runs at the same time
+//     (the hardware deals workgroup ids round-robin over the 8 XCDs) cover a
+//     compact block of output tiles and share A and B rows in their L2;
 //   * the per-channel scale and bias are applied in the fp32 epilogue.
 #include "w8a16_common.h"
 #include "w8a16_internal.h"
@@ -18,8 +25,7 @@
 namespace rf {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kApitch = 72;  // halves per A row in LDS (64 + 8 pad)
+constexpr int kXcds = 8;
 
 struct GemmKernelArgs {
   const _Float16* x;
@@ -32,62 +38,150 @@ struct GemmKernelArgs {
   int M, N, K;
   int kblocks;
   int nstrips;
-  int tiles_n;
+  int tiles_m, tiles_n;
+  int group_m;  // output-tile rows per scheduling group
 };
 
-template <int BM, int BN>
-__global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(GemmKernelArgs a) {
-  constexpr int WM = BM / 2, WN = BN / 2;       // wavefront tile
-  constexpr int TM = WM / 16, TN = WN / 16;     // MFMA tiles per wavefront
-  constexpr int A_CHUNKS = BM * 8 / kThreads;   // 16-byte chunks of A per thread
-  constexpr int B_TILES = BN / 16;
-  constexpr int B_CHUNKS = B_TILES * 64 / kThreads;
-  static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small for 256 threads");
+// Workgroup id -> (tile_m, tile_n).  Ids are first regrouped so that the
+// ids one XCD receives (id % 8 == x) form one contiguous run of tile
+// indices, then the run is walked in groups of `group_m` tile rows,
+// column-major inside a group, so concurrently running workgroups share
+// both A rows (same tile_m) and B strips (same tile_n).
+__device__ __forceinline__ void tile_of(int bid, const GemmKernelArgs& a, int& tm, int& tn) {
+  const int total = a.tiles_m * a.tiles_n;
+  int t = bid;
+  if (total % kXcds == 0) t = (bid % kXcds) * (total / kXcds) + bid / kXcds;
+  const int per_group = a.group_m * a.tiles_n;
+  const int g = t / per_group;
+  const int first_m = g * a.group_m;
+  const int gm = min(a.group_m, a.tiles_m - first_m);
+  const int r = t - g * per_group;
+  tm = first_m + r % gm;
+  tn = r / gm;
+}
 
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kApitch];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][B_TILES * kTileBytes];
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant: global_load_lds_dwordx4 writes each wavefront's
+// 64 x 16 bytes straight into LDS (lane-contiguous), so no VGPRs stage the
+// tiles and STAGES K steps can be in flight.  A rows are unpadded (128 B)
+// and chunk-swizzled instead: LDS chunk slot p of row r holds global chunk
+// p ^ ((r >> 1) & 7), which keeps the 16 rows one 16-lane group reads on
+// 64 distinct banks.  Rows past M and strips past N load clamped (valid)
+// addresses; their results are never stored.  Columns past K (the last K
+// step when K % 64 != 0) are zeroed in LDS after their load lands.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// One global_load_lds_dwordx4: every lane reads 16 bytes at `g`, the
+// wavefront's 64 x 16 bytes land lane-contiguously at LDS byte address
+// `lds` (wave-uniform, passed in M0).  Written as inline asm so the
+// compiler does not serialise every later LDS read behind it (it cannot
+// tell which LDS bytes a DMA writes); the kernel orders the LDS traffic
+// itself with explicit s_waitcnt vmcnt + s_barrier.  Nothing else in these
+// kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Workgroup barrier without the memory fences __syncthreads() implies (a
+// release fence would wait for every DMA in flight).  The caller has
+// already waited for the loads whose data the other wavefronts read.
+__device__ __forceinline__ void barrier_lds() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int KS>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(GemmKernelArgs a) {
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int A_KB = BM * 128;                  // A bytes of one 64-wide K block
+  constexpr int B_TILES = BN / 16;
+  constexpr int B_KB = B_TILES * kTileBytes;      // B bytes of one K block
+  constexpr int A_BYTES = A_KB * KS, B_BYTES = B_KB * KS;
+  constexpr int STAGE = A_BYTES + B_BYTES;        // KS K blocks per stage
+  constexpr int A_LOADS = A_BYTES / (NT * 16);    // per thread per stage
+  constexpr int B_LOADS = B_BYTES / (NT * 16);
+  constexpr int ROWBLKS = BM / 8;                 // 1 KB (8-row) blocks per A K block
+  static_assert(A_LOADS >= 1 && B_LOADS >= 1 && A_LOADS * NT * 16 == A_BYTES &&
+                    B_LOADS * NT * 16 == B_BYTES,
+                "tile does not split into whole 1 KB wavefront loads");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
+  static_assert(TM >= 1 && TN >= 1, "wavefront tile");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int tile_m = blockIdx.x / a.tiles_n;
-  const int tile_n = blockIdx.x % a.tiles_n;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  int tile_m, tile_n;
+  tile_of(blockIdx.x, a, tile_m, tile_n);
   const int m0 = tile_m * BM;
   const int strip0 = tile_n * B_TILES;
+  const int nk = a.kblocks;
+  const int nstage = (nk + KS - 1) / KS;
 
-  uint4 areg[A_CHUNKS], breg[B_CHUNKS];
-
-  auto gload = [&](int kb) {
+  // A load i of this thread: 1 KB block j = wave*A_LOADS + i of the stage,
+  // K block kk = j / ROWBLKS, LDS slot p = (j % ROWBLKS)*64 + lane, row
+  // p/8, global chunk (p%8) ^ ((row>>1)&7).
+  const _Float16* asrc[A_LOADS];
+  int acol[A_LOADS];  // column offset inside the stage's KS*64 columns
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c >> 3, col = (c & 7) * 8;
-      const int m = m0 + row, k = kb * 64 + col;
-      areg[i] = (m < a.M && k < a.K) ? load_u4(a.x + (int64_t)m * a.ldx + k) : make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < A_LOADS; ++i) {
+    const int j = wave * A_LOADS + i;
+    const int kk = j / ROWBLKS;
+    const int p = (j % ROWBLKS) * 64 + lane;
+    const int row = p >> 3;
+    const int chunk = (p & 7) ^ ((row >> 1) & 7);
+    acol[i] = kk * 64 + chunk * 8;
+    const int m = min(m0 + row, a.M - 1);
+    asrc[i] = a.x + (int64_t)m * a.ldx + acol[i];
+  }
+  // B load i: 1 KB block j = K block kk = j / B_TILES, tile t = j % B_TILES.
+  const uint8_t* bsrc[B_LOADS];
+  int bkk[B_LOADS];
+#pragma unroll
+  for (int i = 0; i < B_LOADS; ++i) {
+    const int j = wave * B_LOADS + i;
+    bkk[i] = j / B_TILES;
+    const int strip = min(strip0 + j % B_TILES, a.nstrips - 1);
+    bsrc[i] = a.w + (int64_t)strip * a.kblocks * kTileBytes + lane * 16;
+  }
+  const bool k_tail = (a.K & 63) != 0 || (nk % KS) != 0;
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)smem;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto issue = [&](int st_idx) {
+    const uint32_t st = lds0 + (st_idx % STAGES) * STAGE;
+    const int kcol = st_idx * KS * 64;
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+      // Columns past K would read past the row: load column 0 instead and
+      // zero the slot once it has landed (fix_tail).
+      const _Float16* src = kcol + acol[i] < a.K ? asrc[i] + kcol : asrc[i] - acol[i];
+      dma16(src, st + (wave_u * A_LOADS + i) * 1024);
     }
 #pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int t = c >> 6, l = c & 63;
-      const int strip = strip0 + t;
-      breg[i] = strip < a.nstrips
-                    ? load_u4_stream(a.w + ((int64_t)strip * a.kblocks + kb) * kTileBytes + l * 16)
-                    : make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+    for (int i = 0; i < B_LOADS; ++i) {
+      // K blocks past the weight's last one are clamped; A is zero there.
+      const int kb = min(st_idx * KS + bkk[i], nk - 1);
+      dma16(bsrc[i] + (int64_t)kb * kTileBytes, st + A_BYTES + (wave_u * B_LOADS + i) * 1024);
     }
   };
-  auto sstore = [&](int buf) {
+  auto fix_tail = [&](int st_idx) {
+    uint8_t* st = smem + (st_idx % STAGES) * STAGE;
+    const int kcol = st_idx * KS * 64;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c >> 3, col = (c & 7) * 8;
-      *reinterpret_cast<uint4*>(&As[buf][row * kApitch + col]) = areg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      *reinterpret_cast<uint4*>(&Bs[buf][c * 16]) = breg[i];
-    }
+    for (int i = 0; i < A_LOADS; ++i)
+      if (kcol + acol[i] >= a.K)
+        *reinterpret_cast<uint4*>(st + (wave * A_LOADS + i) * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
   };
 
   floatx4 acc[TM][TN];
@@ -96,40 +190,55 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(GemmKernelArgs a) 
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
-
   const int arow = wm * WM + (lane & 15);
-  const int acol = 16 * (lane >> 4);
-  for (int kb = 0; kb < a.kblocks; ++kb) {
-    const int buf = kb & 1;
-    const bool more = kb + 1 < a.kblocks;
-    if (more) gload(kb + 1);
+  const int sw = (arow >> 1) & 7;  // same for arow + 16*i
+  const int aoff0 = arow * 128 + (((2 * (lane >> 4)) ^ sw) * 16);
+  const int aoff1 = arow * 128 + (((2 * (lane >> 4) + 1) ^ sw) * 16);
 
-    half8 bf[TN][2];
+  auto compute = [&](int st_idx) {
+    const uint8_t* st = smem + (st_idx % STAGES) * STAGE;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const uint4 v = *reinterpret_cast<const uint4*>(&Bs[buf][(wn * TN + j) * kTileBytes + lane * 16]);
-      bf[j][0] = dequant8(v.x, v.y);
-      bf[j][1] = dequant8(v.z, v.w);
+    for (int kk = 0; kk < KS; ++kk) {
+      const uint8_t* sa = st + kk * A_KB;
+      const uint8_t* sb = st + A_BYTES + kk * B_KB;
+      uint4 braw[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        braw[j] = *reinterpret_cast<const uint4*>(sb + (wn * TN + j) * kTileBytes + lane * 16);
+#pragma unroll
+      for (int step = 0; step < 2; ++step) {
+        half8 af[TM], bf[TN];
+        const int aoff = step == 0 ? aoff0 : aoff1;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[i] = *reinterpret_cast<const half8*>(sa + aoff + i * 16 * 128);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bf[j] = step == 0 ? dequant8(braw[j].x, braw[j].y) : dequant8(braw[j].z, braw[j].w);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+      }
     }
-#pragma unroll
-    for (int step = 0; step < 2; ++step) {
-      half8 af[TM];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const half8*>(&As[buf][(arow + 16 * i) * kApitch + acol + 8 * step]);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j][step], acc[i][j]);
-    }
+  };
 
-    if (more) {
-      sstore(buf ^ 1);
-      __syncthreads();
-    }
+  // Prologue: STAGES-1 stages in flight.
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nstage) issue(s);
+  for (int sidx = 0; sidx < nstage; ++sidx) {
+    // Wait for this thread's loads of stage sidx (later stages may stay in
+    // flight), then for everyone's.
+    const int ahead = min(STAGES - 2, nstage - 1 - sidx);  // stages issued after sidx
+    if (ahead >= 2) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (A_LOADS + B_LOADS)) : "memory");
+    else if (ahead == 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(A_LOADS + B_LOADS) : "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (k_tail && sidx == nstage - 1) fix_tail(sidx);
+    barrier_lds();
+    // Everyone is past compute(sidx-1): its stage can be refilled.
+    if (sidx + STAGES - 1 < nstage) issue(sidx + STAGES - 1);
+    compute(sidx);
   }
 
   // Epilogue: lane l holds D[4*(l/16) + r][l%16] of each 16x16 tile.
@@ -150,18 +259,16 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(GemmKernelArgs a) 
   }
 }
 
-}  // namespace
-
-GemmPlan plan_gemm(int M, int N, int /*K*/, const DeviceInfo& /*dev*/) {
-  GemmPlan p;
-  p.bm = 128;
-  p.bn = 128;
-  p.tiles_m = (int)ceil_div(M, p.bm);
-  p.tiles_n = (int)ceil_div(N, p.bn);
-  return p;
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int KS>
+hipError_t launch_dma_t(const GemmKernelArgs& ka, hipStream_t stream) {
+  const int64_t blocks = (int64_t)ka.tiles_m * ka.tiles_n;
+  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((w8a16_gemm_dma_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, KS>),
+                     dim3((unsigned)blocks), dim3(WAVES_M * WAVES_N * 64), 0, stream, ka);
+  return hipGetLastError();
 }
 
-hipError_t launch_gemm(const LinearArgs& a, const GemmPlan& p, hipStream_t stream) {
+GemmKernelArgs make_args(const LinearArgs& a, const GemmPlan& p) {
   GemmKernelArgs ka;
   ka.x = a.x;
   ka.ldx = a.ldx;
@@ -175,15 +282,55 @@ hipError_t launch_gemm(const LinearArgs& a, const GemmPlan& p, hipStream_t strea
   ka.K = a.K;
   ka.kblocks = a.kblocks;
   ka.nstrips = a.nstrips;
+  ka.tiles_m = p.tiles_m;
   ka.tiles_n = p.tiles_n;
-  const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
-  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
-  if (p.bm == 128 && p.bn == 128) {
-    hipLaunchKernelGGL((w8a16_gemm_kernel<128, 128>), dim3((unsigned)blocks), dim3(kThreads), 0,
-                       stream, ka);
-    return hipGetLastError();
+  ka.group_m = p.group_m;
+  return ka;
+}
+
+}  // namespace
+
+// Tile configurations (measured on MI355X over the BASELINE prefill shapes).
+enum GemmCfgId {
+  kM128N128,  // 4 wavefronts 1x4, 3 stages: many tiles (M >= 1024)
+  kM256N256,  // 8 wavefronts 2x4, 2 stages: wide N at moderate M
+  kM64N256,   // 4 wavefronts 1x4, 3 stages: small M
+  kGemmCfgCount
+};
+
+constexpr int kGemmTile[kGemmCfgCount][2] = {{128, 128}, {256, 256}, {64, 256}};
+
+// Kernel choice per shape: the analogue of the reference's W8A16 tile
+// tables (src/ops/rpu_linear_tiling.h:69-127, selectors :544-595), as rules
+// over (M, N) tuned on MI355X.
+GemmPlan plan_gemm(int M, int N, int /*K*/, const DeviceInfo& /*dev*/) {
+  GemmPlan p;
+  int cfg;
+  if ((M >= 768 && N >= 65536) || (M <= 640 && N >= 16384)) {
+    cfg = kM256N256;
+  } else if (M >= 1024) {
+    cfg = kM128N128;
+  } else {
+    cfg = kM64N256;
   }
-  return hipErrorInvalidValue;
+  p.cfg = cfg;
+  p.bm = kGemmTile[cfg][0];
+  p.bn = kGemmTile[cfg][1];
+  p.tiles_m = (int)ceil_div(M, p.bm);
+  p.tiles_n = (int)ceil_div(N, p.bn);
+  p.group_m = cfg == kM256N256 ? 2 : (cfg == kM128N128 && p.tiles_n <= 64 ? 8 : 4);
+  if (p.group_m > p.tiles_m) p.group_m = p.tiles_m;
+  return p;
+}
+
+hipError_t launch_gemm(const LinearArgs& a, const GemmPlan& p, hipStream_t stream) {
+  const GemmKernelArgs ka = make_args(a, p);
+  switch (p.cfg) {
+    case kM128N128: return launch_dma_t<128, 128, 1, 4, 3, 1>(ka, stream);
+    case kM256N256: return launch_dma_t<256, 256, 2, 4, 2, 1>(ka, stream);
+    case kM64N256: return launch_dma_t<64, 256, 1, 4, 3, 1>(ka, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace rf

@@ -36,8 +36,10 @@ struct GemvPlan {
 
 // Prefill GEMM launch plan.
 struct GemmPlan {
+  int cfg;       // tile configuration id (w8a16_gemm.hip)
   int bm, bn;    // workgroup tile
   int tiles_m, tiles_n;
+  int group_m;   // output-tile rows per scheduling group
 };
 
 struct DeviceInfo {

@@ -26,6 +26,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "../../include/w8a16.h"
 
@@ -38,19 +39,25 @@ void check_status(int st, const char* what) {
 int64_t ceil_to(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
 
 // Workspace per (device, stream): allocated through torch's caching
-// allocator, zero-filled once (fill kernel), grown on demand.  The C ABI
-// leaves its counter region zero after every call, and calls on one stream
-// are ordered, so one buffer per stream is safe to reuse.
+// allocator, zero-filled once (fill kernel), at least kMinWorkspace bytes.
+// The C ABI leaves its counter region zero after every call, and calls on
+// one stream are ordered, so one buffer per stream is safe to reuse.  A
+// buffer that has to grow is retired, never freed: a HIP graph captured
+// earlier on that stream may still reference it.
+constexpr int64_t kMinWorkspace = 16 << 20;
+
 struct WorkspaceCache {
   std::mutex mu;
   std::map<std::pair<int, void*>, at::Tensor> bufs;
+  std::vector<at::Tensor> retired;
 
   at::Tensor get(const at::Device& dev, void* stream, size_t bytes) {
     std::lock_guard<std::mutex> g(mu);
     auto key = std::make_pair((int)dev.index(), stream);
     auto it = bufs.find(key);
     if (it != bufs.end() && (size_t)it->second.numel() >= bytes) return it->second;
-    const int64_t sz = ceil_to((int64_t)std::max<size_t>(bytes, 1 << 20), 1 << 20);
+    if (it != bufs.end()) retired.push_back(it->second);
+    const int64_t sz = ceil_to(std::max<int64_t>((int64_t)bytes, kMinWorkspace), 1 << 20);
     at::Tensor t = at::zeros({sz}, at::TensorOptions().dtype(at::kByte).device(dev));
     bufs[key] = t;
     return t;

@@ -355,6 +355,36 @@ def test_op_errors_on_device():
         rf.linear(_to_dev(x), packed, sd, torch.zeros(39, dtype=torch.float16, device=DEV))
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 1024, 8192), (1, 4096, 1024), (300, 384, 1024)])
+def test_graph_capture_replays_match_eager(m, n, k):
+    """The op inside a HIP graph: every replay (with eager work between replays)
+    equals the eager result bit for bit.  (16, 1024, 8192) takes the split-K
+    GEMV path, whose counters must be left zeroed for the next replay."""
+    _say(f"graph capture M={m} N={n} K={k}")
+    x, q, s, b = make_case(m, n, k, seed=17, bias=True)
+    xd, packed, sd, bd = _to_dev(x), rf.pack_weight(_to_dev(q)), _to_dev(s), _to_dev(b)
+    eager = rf.linear(xd, packed, sd, bd)
+    out = torch.empty_like(eager)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        rf.linear_into(xd, packed, sd, bd, out)  # warm-up: workspace for this stream
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        rf.linear_into(xd, packed, sd, bd, out)
+    for i in range(5):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        other = rf.linear(xd, packed, sd, bd)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(other, eager)
+    assert_parity(out.cpu().numpy(), x, q, s, b, label=f"graph {m}x{n}x{k}")
+
+
 def test_w8a16_linear_module_forward():
     torch.manual_seed(0)
     lin = torch.nn.Linear(512, 200, bias=True)
