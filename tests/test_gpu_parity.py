@@ -278,6 +278,44 @@ def test_gemv_every_planner_rule(m, n, k):
     assert (y1.view(np.uint16) == y2.view(np.uint16)).all()
 
 
+# One shape per rule of the GEMM planner (w8a16_gemm.hip plan_gemm).
+GEMM_POLICY = [
+    (100, 520, 1032),    # M < 128: 64x256 tiles
+    (1024, 8200, 264),   # M >= 1024, N >= 8192: 128x256 tiles, 2 workgroups/CU
+    (1100, 1000, 520),   # M >= 1024, N < 8192: 128x128 tiles, 3 workgroups/CU
+    (200, 16400, 136),   # 128 <= M < 1024, N >= 16384: 128x256 tiles
+    (300, 384, 1024),    # 128 <= M < 1024, N < 16384: 128x128 tiles, 3 stages
+]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_POLICY)
+def test_gemm_every_planner_rule(m, n, k):
+    _say(f"gemm policy M={m} N={n} K={k}")
+    x, q, s, b = make_case(m, n, k, seed=18, bias=True)
+    assert rf.select_kernel(m, n, k) == rf.KERNEL_GEMM
+    rows = None if m <= 300 else np.random.default_rng(m).choice(m, 128, replace=False)
+    assert_parity(run_gpu(x, q, s, b), x, q, s, b, rows=rows, label=f"gemm policy {m}x{n}x{k}")
+
+
+def test_gemm_fallback_when_row_stride_overflows_32bit_offsets():
+    """Rows 2**24 + 8 halves apart: the 128-row tile spans more than 4 GB, so the
+    GEMM must take its 64-bit-address kernel; results must not change."""
+    m, n, k = 130, 256, 200
+    ldx = (1 << 24) + 8
+    _say(f"gemm fallback M={m} N={n} K={k} ldx={ldx}")
+    x, q, s, b = make_case(m, n, k, seed=19)
+    big = torch.empty((m - 1) * ldx + k, dtype=torch.float16, device=DEV)
+    view = big.as_strided((m, k), (ldx, 1))
+    view.copy_(_to_dev(x))
+    packed, sd = rf.pack_weight(_to_dev(q)), _to_dev(s)
+    y = rf.linear(view, packed, sd)
+    torch.cuda.synchronize()
+    ref = rf.linear(_to_dev(x), packed, sd)
+    assert torch.equal(y, ref)
+    assert_parity(y.cpu().numpy(), x, q, s, None, label="gemm fallback")
+    del big, view
+
+
 def test_zero_rows_and_extreme_scales():
     n, k = 64, 256
     rng = np.random.default_rng(5)
