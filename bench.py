@@ -2,7 +2,12 @@
 
 Headline (`value`): decode GB/s on BASELINE config 1 -- a Qwen3-8B decoder
 layer's seven W8A16 projections (q, k, v, o, gate, up, down) at batch
-M in {1, 4, 16}.  One step = 21 launches (7 projections x 3 batch sizes).
+M in {1, 4, 16}.  One step computes all 21 projection outputs (7 x 3 batch
+sizes) the way a decoder layer issues them: per batch size, q/k/v in one
+`linear_multi` launch (they share the input, like the reference's fused QKV
+W8A16 kernel), o, gate/up in one `linear_multi` launch, then down -- 12
+launches.  The same step as 21 single-projection launches is reported as
+`config.per_op_GBps`.
 Each batch size's pass reads a different copy of the layer's weights (4
 copies, 772 MB, rotated so the 256 MB Infinity Cache never serves a repeat).
 Inputs are synthetic (weights N(0, 0.02) quantized per channel, activations
@@ -18,7 +23,7 @@ graphs of 40 back-to-back launches, i.e. GPU-side time per launch.
 The same JSON line carries
   * roofline      -- the decode GEMV kernel (every launch in the timed
                      region): algorithmic bytes per launch / average launch
-                     duration (timed region / launches) against the 8 TB/s
+                     duration (timed region / launches, 12 per step) against the 8 TB/s
                      HBM peak; `traffic` is the measured HBM bytes per launch
                      from profiles/gemv_decode_traffic.json when present;
   * prefill       -- BASELINE config 3 (Qwen3-8B MLP prefill, M=2048) in
@@ -154,6 +159,24 @@ def bench_decode(torch, rf, steps, warmup):
     launches = steps * len(DECODE_M) * len(QWEN3_8B)
     step_bytes = sum(nbytes(m, n, k) for m in DECODE_M for _, n, k in QWEN3_8B)
 
+    # The same step with the projections that share an input fused into one
+    # launch each (q/k/v and gate/up; o and down stay single): 4 launches per M.
+    def step_fused(i):
+        for j, m in enumerate(DECODE_M):
+            layer = layers[(i * len(DECODE_M) + j) % LAYER_COPIES]
+            x = xs[m][:, :4096]
+            q, k_, v, o, gate, up, down = layer
+            rf.linear_multi(x, [q[3], k_[3], v[3]], [q[4], k_[4], v[4]])
+            rf.linear_into(x, o[3], o[4], None, outs[(m, 4096)])
+            g, u = rf.linear_multi(x, [gate[3], up[3]], [gate[4], up[4]])
+            rf.linear_into(xs[m][:, :12288], down[3], down[4], None, outs[(m, 4096)])
+
+    for i in range(warmup):
+        step_fused(i)
+    with Timer(torch) as tf:
+        for i in range(steps):
+            step_fused(warmup + i)
+
     rows = []
     for m in DECODE_M:
         for idx, (name, n, k) in enumerate(QWEN3_8B):
@@ -165,19 +188,33 @@ def bench_decode(torch, rf, steps, warmup):
                          "GBps": round(nbytes(m, n, k) / (us * 1e-6) / 1e9, 1),
                          "kernel": "gemv" if rf.select_kernel(m, n, k) == rf.KERNEL_GEMV
                          else "gemm"})
+    for m in DECODE_M:
+        x = xs[m][:, :4096]
+        for name, idxs in (("qkv", (0, 1, 2)), ("gate_up", (4, 5))):
+            copies = [[layer[i] for i in idxs] for layer in layers]
+            us = per_launch_us(torch, lambda c: rf.linear_multi(x, [p[3] for p in c],
+                                                                [p[4] for p in c]), copies, 40)
+            b = sum(nbytes(m, QWEN3_8B[i][1], 4096) - 2 * m * 4096 for i in idxs) + 2 * m * 4096
+            rows.append({"M": m, "proj": name, "N": sum(QWEN3_8B[i][1] for i in idxs), "K": 4096,
+                         "us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                         "kernel": "gemv (one launch)"})
     per_m = {}
     for m in DECODE_M:
-        sel = [r for r in rows if r["M"] == m]
+        sel = [r for r in rows if r["M"] == m and r["proj"] in dict((p, 1) for p, _, _ in QWEN3_8B)]
         per_m[str(m)] = round(sum(nbytes(m, r["N"], r["K"]) for r in sel)
                               / sum(r["us"] * 1e-6 for r in sel) / 1e9, 1)
     del layers
     torch.cuda.empty_cache()
+    fused_launches = steps * len(DECODE_M) * 4
     return {
-        "GBps": step_bytes * steps / (t.ms * 1e-3) / 1e9,
-        "ms_per_step": t.ms / steps,
-        "launches": launches,
-        "avg_launch_us": t.ms * 1e3 / launches,
-        "avg_bytes_per_launch": step_bytes / (len(DECODE_M) * len(QWEN3_8B)),
+        "GBps": step_bytes * steps / (tf.ms * 1e-3) / 1e9,
+        "ms_per_step": tf.ms / steps,
+        "launches": fused_launches,
+        "avg_launch_us": tf.ms * 1e3 / fused_launches,
+        "avg_bytes_per_launch": step_bytes / (len(DECODE_M) * 4),
+        "per_op_GBps": step_bytes * steps / (t.ms * 1e-3) / 1e9,
+        "per_op_ms_per_step": t.ms / steps,
+        "per_op_avg_launch_us": t.ms * 1e3 / launches,
         "per_M_GBps": per_m,
         "per_launch": rows,
     }
@@ -360,7 +397,8 @@ def main():
         del src, dst
     log("decode (cfg1)...")
     dec = bench_decode(torch, rf, args.steps, args.warmup)
-    log(f"decode: {dec['GBps']:.1f} GB/s, {dec['avg_launch_us']:.2f} us/launch")
+    log(f"decode: {dec['GBps']:.1f} GB/s ({dec['avg_launch_us']:.2f} us/launch, q/k/v and "
+        f"gate/up fused); one launch per projection: {dec['per_op_GBps']:.1f} GB/s")
     pre = None
     if not args.no_prefill:
         log("prefill (cfg3)...")
@@ -396,8 +434,12 @@ def main():
             "layer_copies_rotated": LAYER_COPIES,
             "weight_dtype": "int8",
             "per_M_GBps": dec["per_M_GBps"],
-            "launch": "eager torch-op launches on one stream (host enqueue ~5.4 us/call "
-                      "stays ahead of the GPU); per-projection rows replay HIP graphs",
+            "launch": ("per M: q/k/v in one linear_multi launch, o, gate/up in one "
+                       "linear_multi launch, down (12 launches per step); eager torch-op "
+                       "launches on one stream"),
+            "per_op_GBps": round(dec["per_op_GBps"], 1),
+            "per_op_ms_per_step": round(dec["per_op_ms_per_step"], 4),
+            "per_op_note": "the same step as 21 single-projection launches",
         },
         "roofline": {
             "bound": "hbm",

@@ -100,12 +100,29 @@ int rf_w8a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K,
  * (RF_W8A16_KERNEL_GEMV or RF_W8A16_KERNEL_GEMM), or a negative status. */
 int rf_w8a16_select_kernel(int64_t M, int64_t N, int64_t K);
 
-/* Workspace bytes rf_w8a16_linear needs for (M,N,K) with any kernel choice
+/* Up to this many projections share one rf_w8a16_linear_multi launch. */
+#define RF_W8A16_MAX_PROJ 4
+
+/* One projection of rf_w8a16_linear_multi. */
+typedef struct rf_w8a16_proj {
+  const void* w_packed; /* rf_w8a16_packed_bytes(N, K) bytes, layout TILE16X64 */
+  const void* scale;    /* fp16 [N] */
+  const void* bias;     /* fp16 [N] or NULL */
+  void* y;              /* fp16 [M, ldy], ldy >= N */
+  int64_t ldy;
+  int64_t N;
+} rf_w8a16_proj;
+
+/* Workspace bytes rf_w8a16_linear for (M,N,K) with any kernel choice
  * on the current device.  The first RF_W8A16_WS_COUNTER_BYTES bytes are
  * split-K arrival counters: they must be zero before the first call that
  * uses the buffer, and every successful call leaves them zero again. */
 size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 #define RF_W8A16_WS_COUNTER_BYTES 65536
+
+/* Workspace bytes rf_w8a16_linear_multi needs for `count` projections with
+ * output widths Ns[0..count) sharing (M, K); same counter-region contract. */
+size_t rf_w8a16_workspace_bytes_multi(int64_t M, const int64_t* Ns, int32_t count, int64_t K);
 
 /* y = x . dequant(w)^T (+ bias), on `stream` (asynchronous).
  *   x        : fp16 [M, ldx], 16-byte aligned, ldx % 8 == 0, ldx >= K
@@ -126,6 +143,17 @@ int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed,
                     void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                     int32_t kernel, void* workspace, size_t workspace_bytes,
                     void* stream);
+
+/* y_i = x . dequant(w_i)^T (+ b_i) for i < count (1..RF_W8A16_MAX_PROJ),
+ * all sharing x [M, ldx] and K (same constraints as rf_w8a16_linear).  With
+ * the GEMV (M <= 64) all projections run in ONE launch, so x is read once
+ * and the launch ramp is paid once (q/k/v or gate/up of a decoder layer);
+ * otherwise one GEMM launch per projection.  Replaces the fused Q/K/V W8A16
+ * launcher `qkv_parallel_w8a16_multibase` (src/ops/rpu_linear.cpp:1546-1674),
+ * which runs one launch over three weight and scale bases. */
+int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w8a16_proj* projs,
+                          int32_t count, int64_t M, int64_t K, int32_t kernel, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

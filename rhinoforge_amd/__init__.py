@@ -36,6 +36,7 @@ from .ops import (  # noqa: E402
     KERNEL_GEMV,
     linear,
     linear_into,
+    linear_multi,
     pack_weight,
     packed_shape,
     select_kernel,
@@ -54,6 +55,7 @@ __all__ = [
     "dequantize_linear_per_channel",
     "linear",
     "linear_into",
+    "linear_multi",
     "pack_weight",
     "packed_shape",
     "quantize_linear_per_channel",

@@ -26,6 +26,14 @@ KERNEL_AUTO = 0
 KERNEL_GEMV = 1
 KERNEL_GEMM = 2
 WS_COUNTER_BYTES = 65536
+MAX_PROJ = 4
+
+
+class Proj(ctypes.Structure):
+    """struct rf_w8a16_proj (include/w8a16.h)."""
+    _fields_ = [("w_packed", ctypes.c_void_p), ("scale", ctypes.c_void_p),
+                ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("ldy", ctypes.c_int64), ("N", ctypes.c_int64)]
 
 # name -> (restype, argtypes): every entry point declared in include/w8a16.h
 _c = ctypes
@@ -41,6 +49,11 @@ SIGNATURES = {
                                                _c.c_void_p, _c.c_size_t, _c.c_void_p]),
     "rf_w8a16_select_kernel": (_c.c_int, [_c.c_int64, _c.c_int64, _c.c_int64]),
     "rf_w8a16_workspace_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int64]),
+    "rf_w8a16_workspace_bytes_multi": (_c.c_size_t, [_c.c_int64, _c.POINTER(_c.c_int64), _c.c_int32,
+                                                     _c.c_int64]),
+    "rf_w8a16_linear_multi": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int32, _c.POINTER(Proj),
+                                         _c.c_int32, _c.c_int64, _c.c_int64, _c.c_int32,
+                                         _c.c_void_p, _c.c_size_t, _c.c_void_p]),
     "rf_w8a16_linear": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int32,
                                    _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64,
                                    _c.c_int64, _c.c_int64, _c.c_int64, _c.c_int32,

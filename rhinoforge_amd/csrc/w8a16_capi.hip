@@ -187,8 +187,13 @@ int rf_w8a16_select_kernel(int64_t M, int64_t N, int64_t K) {
   return auto_kernel(M);
 }
 
-size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return 0;
+size_t rf_w8a16_workspace_bytes_multi(int64_t M, const int64_t* Ns, int32_t count, int64_t K) {
+  if (!Ns || count < 1 || count > RF_W8A16_MAX_PROJ || M < 1 || M > kMaxDim) return 0;
+  int n32[RF_W8A16_MAX_PROJ];
+  for (int i = 0; i < count; ++i) {
+    if (check_nk(Ns[i], K) != RF_W8A16_OK) return 0;
+    n32[i] = (int)Ns[i];
+  }
   size_t bytes = RF_W8A16_WS_COUNTER_BYTES;
   if (M <= 64) {
     rf::DeviceInfo dev;
@@ -196,25 +201,34 @@ size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
       dev.cus = 256;
       dev.gfx950 = false;
     }
-    const rf::GemvPlan p = rf::plan_gemv((int)M, (int)N, (int)K, dev);
-    bytes += rf::gemv_workspace_bytes(p, (int)M, (int)N);
+    const rf::GemvPlan p = rf::plan_gemv((int)M, n32, count, (int)K, dev);
+    bytes += rf::gemv_workspace_bytes(p, (int)M, n32, count);
   }
   return bytes;
 }
 
-int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed, int32_t layout,
-                    const void* scale, const void* bias, void* y, int64_t ldy, int64_t M,
-                    int64_t N, int64_t K, int32_t kernel, void* workspace,
-                    size_t workspace_bytes, void* stream) {
-  if (!x || !w_packed || !scale || !y) return RF_W8A16_EINVAL;
-  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return RF_W8A16_EINVAL;
-  if (ldx < K || ldy < N) return RF_W8A16_EINVAL;
+size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return rf_w8a16_workspace_bytes_multi(M, &N, 1, K);
+}
+
+int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w8a16_proj* projs,
+                          int32_t count, int64_t M, int64_t K, int32_t kernel, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (!x || !projs || count < 1 || count > RF_W8A16_MAX_PROJ) return RF_W8A16_EINVAL;
+  if (M < 1 || M > kMaxDim || K < 1 || K > kMaxDim || ldx < K) return RF_W8A16_EINVAL;
+  for (int i = 0; i < count; ++i) {
+    const rf_w8a16_proj& q = projs[i];
+    if (!q.w_packed || !q.scale || !q.y) return RF_W8A16_EINVAL;
+    if (check_nk(q.N, K) != RF_W8A16_OK || q.ldy < q.N) return RF_W8A16_EINVAL;
+  }
   if (layout != RF_W8A16_LAYOUT_TILE16X64) return RF_W8A16_ELAYOUT;
   if (K % 8 != 0 || ldx % 8 != 0 || !aligned(x, 16)) return RF_W8A16_EALIGN;
-  if (!aligned(w_packed, 16) || !aligned(scale, 2) || !aligned(y, 2) ||
-      (bias && !aligned(bias, 2)))
-    return RF_W8A16_EALIGN;
-  if ((N + 15) / 16 > 0x7fffffff / 1 || (K + 63) / 64 > 0x7fffffff) return RF_W8A16_EINVAL;
+  for (int i = 0; i < count; ++i) {
+    const rf_w8a16_proj& q = projs[i];
+    if (!aligned(q.w_packed, 16) || !aligned(q.scale, 2) || !aligned(q.y, 2) ||
+        (q.bias && !aligned(q.bias, 2)))
+      return RF_W8A16_EALIGN;
+  }
 
   rf::DeviceInfo dev;
   int st = rf::device_info(&dev);
@@ -224,36 +238,69 @@ int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed, int32_t la
   if (kernel == RF_W8A16_KERNEL_AUTO) kernel = auto_kernel(M);
   if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
   if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
-
-  rf::LinearArgs a;
-  a.x = static_cast<const _Float16*>(x);
-  a.ldx = ldx;
-  a.w = static_cast<const uint8_t*>(w_packed);
-  a.scale = static_cast<const _Float16*>(scale);
-  a.bias = static_cast<const _Float16*>(bias);
-  a.y = static_cast<_Float16*>(y);
-  a.ldy = ldy;
-  a.M = (int)M;
-  a.N = (int)N;
-  a.K = (int)K;
-  a.kblocks = (int)ceil_div(K, 64);
-  a.nstrips = (int)ceil_div(N, 16);
   hipStream_t s = static_cast<hipStream_t>(stream);
 
-  hipError_t e;
   if (kernel == RF_W8A16_KERNEL_GEMV) {
-    const rf::GemvPlan p = rf::plan_gemv(a.M, a.N, a.K, dev);
+    rf::GemvProblem pr;
+    pr.x = static_cast<const _Float16*>(x);
+    pr.ldx = ldx;
+    pr.M = (int)M;
+    pr.K = (int)K;
+    pr.nproj = count;
+    int n32[RF_W8A16_MAX_PROJ];
+    for (int i = 0; i < count; ++i) {
+      rf::GemvProjection& d = pr.proj[i];
+      d.w = static_cast<const uint8_t*>(projs[i].w_packed);
+      d.scale = static_cast<const _Float16*>(projs[i].scale);
+      d.bias = static_cast<const _Float16*>(projs[i].bias);
+      d.y = static_cast<_Float16*>(projs[i].y);
+      d.ldy = projs[i].ldy;
+      d.N = (int)projs[i].N;
+      n32[i] = d.N;
+    }
+    const rf::GemvPlan p = rf::plan_gemv(pr.M, n32, count, pr.K, dev);
     if (p.splits > 1) {
-      const size_t need = RF_W8A16_WS_COUNTER_BYTES + rf::gemv_workspace_bytes(p, a.M, a.N);
+      const size_t need = RF_W8A16_WS_COUNTER_BYTES + rf::gemv_workspace_bytes(p, pr.M, n32, count);
       if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
         return RF_W8A16_EWORKSPACE;
     }
-    e = rf::launch_gemv(a, p, p.splits > 1 ? workspace : nullptr, s);
-  } else {
-    const rf::GemmPlan p = rf::plan_gemm(a.M, a.N, a.K, dev);
-    e = rf::launch_gemm(a, p, s);
+    const hipError_t e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);
+    return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
   }
-  return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
+  for (int i = 0; i < count; ++i) {
+    rf::LinearArgs a;
+    a.x = static_cast<const _Float16*>(x);
+    a.ldx = ldx;
+    a.w = static_cast<const uint8_t*>(projs[i].w_packed);
+    a.scale = static_cast<const _Float16*>(projs[i].scale);
+    a.bias = static_cast<const _Float16*>(projs[i].bias);
+    a.y = static_cast<_Float16*>(projs[i].y);
+    a.ldy = projs[i].ldy;
+    a.M = (int)M;
+    a.N = (int)projs[i].N;
+    a.K = (int)K;
+    a.kblocks = (int)ceil_div(K, 64);
+    a.nstrips = (int)ceil_div(a.N, 16);
+    const rf::GemmPlan p = rf::plan_gemm(a.M, a.N, a.K, dev);
+    const hipError_t e = rf::launch_gemm(a, p, s);
+    if (e != hipSuccess) return RF_W8A16_EHIP;
+  }
+  return RF_W8A16_OK;
+}
+
+int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed, int32_t layout,
+                    const void* scale, const void* bias, void* y, int64_t ldy, int64_t M,
+                    int64_t N, int64_t K, int32_t kernel, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  rf_w8a16_proj q;
+  q.w_packed = w_packed;
+  q.scale = scale;
+  q.bias = bias;
+  q.y = y;
+  q.ldy = ldy;
+  q.N = N;
+  return rf_w8a16_linear_multi(x, ldx, layout, &q, 1, M, K, kernel, workspace, workspace_bytes,
+                               stream);
 }
 
 }  // extern "C"

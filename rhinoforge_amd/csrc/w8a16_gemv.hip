@@ -38,22 +38,34 @@ namespace rf {
 namespace {
 
 constexpr int kMaxSplits = 16;
+constexpr int kMaxProj = RF_W8A16_MAX_PROJ;
 constexpr int kMaxGroupsSplit = RF_W8A16_WS_COUNTER_BYTES / 4;
 
-struct GemvKernelArgs {
-  const _Float16* x;
-  int64_t ldx;
+// One weight matrix of a launch.  Several projections that share the
+// activation x (q/k/v, or gate/up) run in one launch: workgroups are
+// numbered projection-major, projection p owning groups [group0, next group0).
+struct GemvProj {
   const uint8_t* w;
   const _Float16* scale;
   const _Float16* bias;
   _Float16* y;
   int64_t ldy;
-  int M, N, K;
-  int kblocks;
+  int N;
   int nstrips;
+  int group0;  // first workgroup (blockIdx.x) of this projection
+  int col0;    // first column of this projection in the partial buffer
+};
+
+struct GemvKernelArgs {
+  const _Float16* x;
+  int64_t ldx;
+  int M, K;
+  int kblocks;
+  int nproj;
+  GemvProj proj[kMaxProj];
   int splits;
   int kb_per_split;
-  int np;              // padded N (nstrips * 16), row stride of partials
+  int np;              // padded columns of all projections: row stride of partials
   float* partial;      // [splits][M][np]
   uint32_t* counters;  // [groups]
 };
@@ -124,7 +136,20 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   const int wave = tid >> 6;
   const int group = blockIdx.x;
   const int split = blockIdx.y;
-  const int strip0 = group * NS;
+  // Projection of this workgroup (uniform across it).
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProj; ++i)
+    if (i < a.nproj && group >= a.proj[i].group0) pi = i;
+  const uint8_t* const P_w = a.proj[pi].w;
+  const _Float16* const P_scale = a.proj[pi].scale;
+  const _Float16* const P_bias = a.proj[pi].bias;
+  _Float16* const P_y = a.proj[pi].y;
+  const int64_t P_ldy = a.proj[pi].ldy;
+  const int P_N = a.proj[pi].N;
+  const int P_nstrips = a.proj[pi].nstrips;
+  const int P_col0 = a.proj[pi].col0;
+  const int strip0 = (group - a.proj[pi].group0) * NS;
   const int kb0 = split * a.kb_per_split;
   const int kb1 = min(kb0 + a.kb_per_split, a.kblocks);
   const int ntiles = kb1 - kb0;
@@ -155,8 +180,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   const uint8_t* wbase[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    strip_ok[s] = (strip0 + s) < a.nstrips;
-    wbase[s] = a.w + ((int64_t)(strip0 + s) * a.kblocks + kb0) * kTileBytes + lane * 16;
+    strip_ok[s] = (strip0 + s) < P_nstrips;
+    wbase[s] = P_w + ((int64_t)(strip0 + s) * a.kblocks + kb0) * kTileBytes + lane * 16;
   }
 
   // Tiles of this wavefront: local index kl = wave + W*i, i in [0, my).
@@ -243,15 +268,15 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
     const int mt = t / NS, s = t % NS;
     const int n = (strip0 + s) * 16 + (ln & 15);
     const int m = mt * 16 + 4 * (ln >> 4) + r;
-    if (m >= a.M || strip0 + s >= a.nstrips) continue;
+    if (m >= a.M || strip0 + s >= P_nstrips) continue;
     if (a.splits == 1) {
-      if (n < a.N) {
-        const float sc = (float)a.scale[n];
-        const float bi = a.bias ? (float)a.bias[n] : 0.f;
-        a.y[(int64_t)m * a.ldy + n] = (_Float16)__builtin_fmaf(sum, sc, bi);
+      if (n < P_N) {
+        const float sc = (float)P_scale[n];
+        const float bi = P_bias ? (float)P_bias[n] : 0.f;
+        P_y[(int64_t)m * P_ldy + n] = (_Float16)__builtin_fmaf(sum, sc, bi);
       }
     } else {
-      store_coherent(&a.partial[((int64_t)split * a.M + m) * a.np + n], sum);
+      store_coherent(&a.partial[((int64_t)split * a.M + m) * a.np + P_col0 + n], sum);
     }
   }
   if (a.splits == 1) return;
@@ -268,7 +293,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   __syncthreads();
   if (!is_last) return;
 
-  const int nrows = min(NS, a.nstrips - strip0) * 16;
+  const int nrows = min(NS, P_nstrips - strip0) * 16;
   const int total = a.M * nrows;
   for (int i = tid; i < total; i += kThreads) {
     const int m = i / nrows;
@@ -278,15 +303,17 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
     float part[kMaxSplits];
 #pragma unroll
     for (int sp = 0; sp < kMaxSplits; ++sp)
-      part[sp] = sp < a.splits ? load_coherent(&a.partial[((int64_t)sp * a.M + m) * a.np + n]) : 0.f;
+      part[sp] = sp < a.splits
+                     ? load_coherent(&a.partial[((int64_t)sp * a.M + m) * a.np + P_col0 + n])
+                     : 0.f;
     float sum = part[0];
 #pragma unroll
     for (int sp = 1; sp < kMaxSplits; ++sp)
       if (sp < a.splits) sum += part[sp];
-    if (n < a.N) {
-      const float sc = (float)a.scale[n];
-      const float bi = a.bias ? (float)a.bias[n] : 0.f;
-      a.y[(int64_t)m * a.ldy + n] = (_Float16)__builtin_fmaf(sum, sc, bi);
+    if (n < P_N) {
+      const float sc = (float)P_scale[n];
+      const float bi = P_bias ? (float)P_bias[n] : 0.f;
+      P_y[(int64_t)m * P_ldy + n] = (_Float16)__builtin_fmaf(sum, sc, bi);
     }
   }
   if (tid == 0)
@@ -303,23 +330,37 @@ hipError_t launch_t(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t str
   return hipGetLastError();
 }
 
-GemvKernelArgs make_args(const LinearArgs& a, const GemvPlan& p, void* workspace) {
+GemvKernelArgs make_args(const GemvProblem& pr, const GemvPlan& p, void* workspace) {
   GemvKernelArgs ka;
-  ka.x = a.x;
-  ka.ldx = a.ldx;
-  ka.w = a.w;
-  ka.scale = a.scale;
-  ka.bias = a.bias;
-  ka.y = a.y;
-  ka.ldy = a.ldy;
-  ka.M = a.M;
-  ka.N = a.N;
-  ka.K = a.K;
-  ka.kblocks = a.kblocks;
-  ka.nstrips = a.nstrips;
+  ka.x = pr.x;
+  ka.ldx = pr.ldx;
+  ka.M = pr.M;
+  ka.K = pr.K;
+  ka.kblocks = (int)ceil_div(pr.K, 64);
+  ka.nproj = pr.nproj;
+  int group = 0, col = 0;
+  for (int i = 0; i < kMaxProj; ++i) {
+    GemvProj& q = ka.proj[i];
+    if (i < pr.nproj) {
+      q.w = pr.proj[i].w;
+      q.scale = pr.proj[i].scale;
+      q.bias = pr.proj[i].bias;
+      q.y = pr.proj[i].y;
+      q.ldy = pr.proj[i].ldy;
+      q.N = pr.proj[i].N;
+      q.nstrips = (int)ceil_div(pr.proj[i].N, 16);
+      q.group0 = group;
+      q.col0 = col;
+      group += (int)ceil_div(q.nstrips, p.ns);
+      col += q.nstrips * 16;
+    } else {
+      q = ka.proj[0];
+      q.group0 = 0x7fffffff;  // never selected
+    }
+  }
   ka.splits = p.splits;
   ka.kb_per_split = p.kb_per_split;
-  ka.np = a.nstrips * 16;
+  ka.np = col;
   // Workspace: [counters | partials]; counter region size fixed by the ABI.
   ka.counters = reinterpret_cast<uint32_t*>(workspace);
   ka.partial = workspace ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
@@ -338,6 +379,8 @@ enum GemvCfgId {
   kG1x2W16U2,   // MT=1 NS=2 W=16 U=2
   kG1x4W8U2,    // MT=1 NS=4 W=8  U=2   (M 5..16: x fragment reused 4x)
   kG1x4W4U2,    // MT=1 NS=4 W=4  U=2
+  kG1x2W8U2,    // MT=1 NS=2 W=8  U=2
+  kG1x2W4U4,    // MT=1 NS=2 W=4  U=4
   kG2x4W4U2,    // MT=2 NS=4 W=4  U=2
   kG2x2W8U1,    // MT=2 NS=2 W=8  U=1
   kG2x1W8U4,    // MT=2 NS=1 W=8  U=4
@@ -353,7 +396,8 @@ struct GemvCfgDesc {
 
 constexpr GemvCfgDesc kGemvCfgs[kGemvCfgCount] = {
     {1, 1, 16, false}, {1, 1, 16, false}, {1, 1, 8, true}, {1, 1, 4, false},
-    {1, 2, 16, false}, {1, 4, 8, false},  {1, 4, 4, false}, {2, 4, 4, false},
+    {1, 2, 16, false}, {1, 4, 8, false},  {1, 4, 4, false}, {1, 2, 8, false},
+    {1, 2, 4, false},  {2, 4, 4, false},
     {2, 2, 8, false},  {2, 1, 8, false},  {4, 2, 8, false}, {4, 2, 4, false},
 };
 
@@ -364,15 +408,17 @@ bool lds_fits(int cfg, int M, int kb_per_split) {
 
 }  // namespace
 
-size_t gemv_workspace_bytes(const GemvPlan& p, int M, int N) {
+size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj) {
   if (p.splits <= 1) return 0;
-  const int64_t np = round_up(N, 16);
+  int64_t np = 0;
+  for (int i = 0; i < nproj; ++i) np += round_up(Ns[i], 16);
   return (size_t)p.splits * (size_t)M * (size_t)np * sizeof(float);
 }
 
-hipError_t launch_gemv(const LinearArgs& a, const GemvPlan& p, void* workspace,
+hipError_t launch_gemv(const GemvProblem& pr, const GemvPlan& p, void* workspace,
                        hipStream_t stream) {
-  const GemvKernelArgs ka = make_args(a, p, workspace);
+  if (pr.nproj < 1 || pr.nproj > kMaxProj) return hipErrorInvalidValue;
+  const GemvKernelArgs ka = make_args(pr, p, workspace);
   switch (p.cfg) {
     case kG1x1W16U4: return launch_t<1, 1, 16, 4, false, true>(ka, p, stream);
     case kG1x1W16U2: return launch_t<1, 1, 16, 2, false, true>(ka, p, stream);
@@ -381,6 +427,8 @@ hipError_t launch_gemv(const LinearArgs& a, const GemvPlan& p, void* workspace,
     case kG1x2W16U2: return launch_t<1, 2, 16, 2, false, true>(ka, p, stream);
     case kG1x4W8U2: return launch_t<1, 4, 8, 2, false, true>(ka, p, stream);
     case kG1x4W4U2: return launch_t<1, 4, 4, 2, false, true>(ka, p, stream);
+    case kG1x2W8U2: return launch_t<1, 2, 8, 2, false, true>(ka, p, stream);
+    case kG1x2W4U4: return launch_t<1, 2, 4, 4, false, true>(ka, p, stream);
     case kG2x4W4U2: return launch_t<2, 4, 4, 2, false, true>(ka, p, stream);
     case kG2x2W8U1: return launch_t<2, 2, 8, 1, false, true>(ka, p, stream);
     case kG2x1W8U4: return launch_t<2, 1, 8, 4, false, true>(ka, p, stream);
@@ -399,8 +447,10 @@ hipError_t launch_gemv(const LinearArgs& a, const GemvPlan& p, void* workspace,
 //     strips share it when there are enough strips to fill the chip;
 //   * M 17..64: two / four 16-row m-tiles per wavefront;
 //   * K splits only where the strips alone cannot fill 256 CUs.
-GemvPlan plan_gemv(int M, int N, int K, const DeviceInfo& dev) {
-  const int nstrips = (int)ceil_div(N, 16);
+GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev) {
+  // Rules see the launch's strips of all projections together.
+  int nstrips = 0;
+  for (int i = 0; i < nproj; ++i) nstrips += (int)ceil_div(Ns[i], 16);
   const int kblocks = (int)ceil_div(K, 64);
   // Thresholds are in strips for a 256-CU part; scale for smaller parts.
   const int cu = dev.cus > 0 ? dev.cus : 256;
@@ -408,7 +458,9 @@ GemvPlan plan_gemv(int M, int N, int K, const DeviceInfo& dev) {
   int cfg, splits = 1;
   if (M <= 4) {
     if (strips_ge(640)) {
-      cfg = kG1x1W8U4XL;
+      // Many strips: x staged in LDS at M <= 2; two strips per workgroup
+      // sharing the fragment at M 3..4 once there are >= 1024 strips.
+      cfg = (M >= 3 && strips_ge(1024)) ? kG1x2W4U4 : kG1x1W8U4XL;
       if (!lds_fits(cfg, M, kblocks)) cfg = kG1x1W4U4;
     } else if (strips_ge(257)) {
       cfg = kG1x2W16U2;
@@ -420,8 +472,12 @@ GemvPlan plan_gemv(int M, int N, int K, const DeviceInfo& dev) {
   } else if (M <= 16) {
     if (strips_ge(2048)) {
       cfg = kG1x4W4U2;
+    } else if (strips_ge(1024)) {
+      cfg = kG1x2W8U2;
     } else if (strips_ge(512)) {
       cfg = kG1x4W8U2;
+    } else if (strips_ge(257)) {
+      cfg = kG1x2W8U2;
     } else if (kblocks >= 128) {
       cfg = kG1x4W8U2;
       splits = 4;
@@ -455,7 +511,8 @@ GemvPlan plan_gemv(int M, int N, int K, const DeviceInfo& dev) {
   p.cfg = cfg;
   p.mt = kGemvCfgs[cfg].mt;
   p.ns = kGemvCfgs[cfg].ns;
-  p.groups = (int)ceil_div(nstrips, p.ns);
+  p.groups = 0;
+  for (int i = 0; i < nproj; ++i) p.groups += (int)ceil_div(ceil_div(Ns[i], 16), p.ns);
   if (p.groups > kMaxGroupsSplit) splits = 1;  // counter region holds kMaxGroupsSplit counters
   if (splits > kblocks) splits = kblocks;
   p.kb_per_split = (int)ceil_div(kblocks, splits);

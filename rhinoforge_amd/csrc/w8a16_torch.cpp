@@ -5,6 +5,8 @@
 //          int layout=1, int kernel=0) -> Tensor
 //   linear_into(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias,
 //               Tensor(a!) out, int layout=1, int kernel=0) -> ()
+//   linear_multi(Tensor input, Tensor[] weights, Tensor[] weight_scales,
+//                Tensor?[] biases, int layout=1, int kernel=0) -> Tensor[]
 //   pack_weight(Tensor q) -> Tensor
 //   unpack_weight(Tensor packed, int N, int K) -> Tensor
 //   select_kernel(int M, int N, int K) -> int
@@ -166,6 +168,67 @@ void linear_into_hip(const at::Tensor& input, const at::Tensor& weight, const at
   launch(c, weight, scale, bias, y2, layout, kernel, "w8a16::linear_into");
 }
 
+// Several projections sharing the input (q/k/v, gate/up): one GEMV launch
+// for decode-sized M.  Outputs are fresh tensors [..., N_i].
+std::vector<at::Tensor> linear_multi_hip(const at::Tensor& input, at::TensorList weights,
+                                         at::TensorList scales,
+                                         const c10::List<c10::optional<at::Tensor>>& biases,
+                                         int64_t layout, int64_t kernel) {
+  RECORD_FUNCTION("w8a16::linear_multi", {});
+  const char* op = "w8a16::linear_multi";
+  const int64_t count = (int64_t)weights.size();
+  TORCH_CHECK(count >= 1 && count <= RF_W8A16_MAX_PROJ, op, ": between 1 and ",
+              RF_W8A16_MAX_PROJ, " projections, got ", count);
+  TORCH_CHECK((int64_t)scales.size() == count, op, ": ", count, " weights but ", scales.size(),
+              " weight_scales");
+  TORCH_CHECK(biases.size() == 0 || (int64_t)biases.size() == count, op, ": ", count,
+              " weights but ", biases.size(), " biases");
+  std::vector<c10::optional<at::Tensor>> b(count);
+  for (int64_t i = 0; i < (int64_t)biases.size(); ++i) b[i] = biases.get(i);
+  std::vector<Checked> cs;
+  for (int64_t i = 0; i < count; ++i) cs.push_back(check_args(input, weights[i], scales[i], b[i], layout, op));
+  const Checked& c0 = cs[0];
+  std::vector<at::Tensor> outs;
+  std::vector<rf_w8a16_proj> projs(count);
+  std::vector<int64_t> Ns(count);
+  for (int64_t i = 0; i < count; ++i) {
+    at::Tensor y2 = at::empty({c0.M, cs[i].N}, input.options());
+    projs[i].w_packed = weights[i].data_ptr();
+    projs[i].scale = scales[i].data_ptr();
+    projs[i].bias = (b[i].has_value() && b[i]->defined()) ? b[i]->data_ptr() : nullptr;
+    projs[i].y = y2.data_ptr();
+    projs[i].ldy = y2.stride(0);
+    projs[i].N = cs[i].N;
+    Ns[i] = cs[i].N;
+    outs.push_back(y2);
+  }
+  if (c0.M > 0) {
+    c10::DeviceGuard guard(c0.x2.device());
+    void* stream = c10::hip::getCurrentHIPStream(c0.x2.device().index()).stream();
+    const size_t ws_bytes = rf_w8a16_workspace_bytes_multi(c0.M, Ns.data(), (int32_t)count, c0.K);
+    TORCH_CHECK(ws_bytes > 0, op, ": ", rf_w8a16_status_str(RF_W8A16_EINVAL));
+    at::Tensor ws = workspace_cache().get(c0.x2.device(), stream, ws_bytes);
+    const int st = rf_w8a16_linear_multi(c0.x2.data_ptr(), c0.x2.stride(0), (int32_t)layout,
+                                         projs.data(), (int32_t)count, c0.M, c0.K,
+                                         (int32_t)kernel, ws.data_ptr(), (size_t)ws.numel(),
+                                         stream);
+    check_status(st, op);
+  }
+  for (int64_t i = 0; i < count; ++i) {
+    std::vector<int64_t> shape = input.sizes().vec();
+    shape.back() = cs[i].N;
+    outs[i] = outs[i].view(shape);
+  }
+  return outs;
+}
+
+std::vector<at::Tensor> linear_multi_cpu(const at::Tensor&, at::TensorList, at::TensorList,
+                                         const c10::List<c10::optional<at::Tensor>>&, int64_t,
+                                         int64_t) {
+  TORCH_CHECK(false, "w8a16::linear_multi: tensors are on the CPU; the W8A16 kernels run on a "
+              "HIP device (gfx950) only and there is no CPU implementation");
+}
+
 at::Tensor linear_meta(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
                        const c10::optional<at::Tensor>& bias, int64_t layout, int64_t kernel) {
   std::vector<int64_t> shape = input.sizes().vec();
@@ -243,6 +306,8 @@ TORCH_LIBRARY(w8a16, m) {
         "int layout=1, int kernel=0) -> Tensor");
   m.def("linear_into(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias, "
         "Tensor(a!) out, int layout=1, int kernel=0) -> ()");
+  m.def("linear_multi(Tensor input, Tensor[] weights, Tensor[] weight_scales, Tensor?[] biases, "
+        "int layout=1, int kernel=0) -> Tensor[]");
   m.def("pack_weight(Tensor q) -> Tensor", TORCH_FN(pack_weight));
   m.def("unpack_weight(Tensor packed, int N, int K) -> Tensor", TORCH_FN(unpack_weight));
   m.def("select_kernel(int M, int N, int K) -> int", TORCH_FN(select_kernel));
@@ -252,6 +317,7 @@ TORCH_LIBRARY(w8a16, m) {
 TORCH_LIBRARY_IMPL(w8a16, CUDA, m) {
   m.impl("linear", TORCH_FN(linear_hip));
   m.impl("linear_into", TORCH_FN(linear_into_hip));
+  m.impl("linear_multi", TORCH_FN(linear_multi_hip));
 }
 
 TORCH_LIBRARY_IMPL(w8a16, Meta, m) { m.impl("linear", TORCH_FN(linear_meta)); }
@@ -259,4 +325,5 @@ TORCH_LIBRARY_IMPL(w8a16, Meta, m) { m.impl("linear", TORCH_FN(linear_meta)); }
 TORCH_LIBRARY_IMPL(w8a16, CPU, m) {
   m.impl("linear", TORCH_FN(linear_cpu));
   m.impl("linear_into", TORCH_FN(linear_into_cpu));
+  m.impl("linear_multi", TORCH_FN(linear_multi_cpu));
 }

@@ -56,6 +56,22 @@ def linear_into(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.T
     torch.ops.w8a16.linear_into(input, weight, weight_scale, bias, out, layout, kernel)
 
 
+def linear_multi(input: torch.Tensor, weights, weight_scales, biases=None, *,
+                 layout: int = LAYOUT_TILE16X64, kernel: int = KERNEL_AUTO) -> list:
+    """Several projections of one input (q/k/v, gate/up) in one decode launch.
+
+    Returns [input . (s_i (.) q_i)^T (+ b_i)] for each (weight_i, weight_scale_i,
+    bias_i).  With M <= 64 all projections run in a single GEMV launch (the
+    analogue of the reference's fused QKV W8A16 kernel,
+    src/ops/rpu_linear.cpp:1546-1674); larger M runs one GEMM per projection.
+    """
+    weights = list(weights)
+    if biases is None:
+        biases = [None] * len(weights)
+    return torch.ops.w8a16.linear_multi(input, weights, list(weight_scales), list(biases),
+                                        layout, kernel)
+
+
 def select_kernel(m: int, n: int, k: int) -> int:
     """Kernel the AUTO policy runs for (M, N, K): KERNEL_GEMV or KERNEL_GEMM."""
     return int(torch.ops.w8a16.select_kernel(m, n, k))

@@ -249,11 +249,14 @@ def test_edge_shapes(m, n, k, bias):
 GEMV_POLICY = [
     (2, 10240, 512),   # M<=4, >=640 strips: x staged in LDS
     (4, 10240, 8256),  # same rule, x does not fit in LDS: plain 4-wave config
+    (3, 16384, 512),   # M 3..4, >=1024 strips: two strips per 4-wave workgroup
     (1, 5000, 320),    # M<=4, 257..639 strips: two strips per workgroup
     (3, 512, 8192),    # M<=4, long K
     (1, 512, 1024),    # M<=4, default
     (8, 32768, 128),   # M 5..16, >=2048 strips
+    (16, 16384, 256),  # M 5..16, >=1024 strips: two strips per 8-wave workgroup
     (12, 8192, 256),   # M 5..16, >=512 strips
+    (10, 5000, 512),   # M 5..16, 257..511 strips: two strips per 8-wave workgroup
     (16, 1024, 8192),  # M 5..16, long K: 4-way K split
     (9, 1000, 1024),   # M 5..16, <=64 strips: 4-way K split
     (16, 2048, 1024),  # M 5..16, default
@@ -421,6 +424,65 @@ def test_graph_capture_replays_match_eager(m, n, k):
         torch.cuda.synchronize()
         assert torch.equal(other, eager)
     assert_parity(out.cpu().numpy(), x, q, s, b, label=f"graph {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 40, 100])
+def test_linear_multi_qkv_and_gate_up(m):
+    """q/k/v (4096/1024/1024 x 4096, q with a bias) and gate/up (12288 x 4096) in one
+    call each: every output against the oracle, and against separate calls."""
+    groups = [[(4096, True), (1024, False), (1024, False)], [(12288, False), (12288, False)]]
+    k = 4096
+    for gi, group in enumerate(groups):
+        _say(f"linear_multi M={m} group {gi}")
+        x = o.make_activation(o.derive_seed(20, "x", m, gi), m, k)
+        cases = []
+        for pi, (n, has_bias) in enumerate(group):
+            q, s = make_weights(n, k, seed=200 + 10 * gi + pi)
+            b = (o.normal(o.derive_seed(21, "b", n, pi), (n,)) * 0.1).astype(np.float16) if has_bias else None
+            cases.append((q, s, b, rf.pack_weight(_to_dev(q))))
+        xd = _to_dev(x)
+        ys = rf.linear_multi(xd, [c[3] for c in cases], [_to_dev(c[1]) for c in cases],
+                             [None if c[2] is None else _to_dev(c[2]) for c in cases])
+        torch.cuda.synchronize()
+        for pi, (q, s, b, packed) in enumerate(cases):
+            y = ys[pi].cpu().numpy()
+            assert_parity(y, x, q, s, b, label=f"multi M={m} g{gi} p{pi}")
+            single = rf.linear(xd, packed, _to_dev(s), None if b is None else _to_dev(b)).cpu().numpy()
+            rep = o.check_tolerance(y, single, o.oracle_fp64(x, q, s, b))
+            assert rep.ok, f"multi vs single: {rep}"
+
+
+def test_linear_multi_split_k_and_capi():
+    """M=16, K=12288: the shared launch takes the 4-way K split; also via ctypes."""
+    m, k = 16, 12288
+    ns = [1024, 512, 256]
+    x = o.make_activation(22, m, k)
+    cases = []
+    for pi, n in enumerate(ns):
+        q, s = make_weights(n, k, seed=230 + pi)
+        cases.append((q, s, rf.pack_weight(_to_dev(q)), _to_dev(s)))
+    xd = _to_dev(x)
+    ys = rf.linear_multi(xd, [c[2] for c in cases], [c[3] for c in cases])
+    again = rf.linear_multi(xd, [c[2] for c in cases], [c[3] for c in cases])
+    torch.cuda.synchronize()
+    for pi, (q, s, _, _) in enumerate(cases):
+        assert torch.equal(ys[pi], again[pi])
+        assert_parity(ys[pi].cpu().numpy(), x, q, s, None, label=f"multi split-K p{pi}")
+    lib = capi.load()
+    outs = [torch.empty(m, n, dtype=torch.float16, device=DEV) for n in ns]
+    arr = (capi.Proj * len(ns))()
+    for i, (c, y) in enumerate(zip(cases, outs)):
+        arr[i] = capi.Proj(c[2].data_ptr(), c[3].data_ptr(), None, y.data_ptr(), ns[i], ns[i])
+    nsc = (ctypes.c_int64 * len(ns))(*ns)
+    ws_bytes = lib.rf_w8a16_workspace_bytes_multi(m, nsc, len(ns), k)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=DEV)
+    st = lib.rf_w8a16_linear_multi(xd.data_ptr(), k, capi.LAYOUT_TILE16X64, arr, len(ns), m, k,
+                                   capi.KERNEL_AUTO, ws.data_ptr(), ws_bytes,
+                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    capi.check(st, "rf_w8a16_linear_multi")
+    torch.cuda.synchronize()
+    for y, ref in zip(outs, ys):
+        assert torch.equal(y, ref)
 
 
 def test_w8a16_linear_module_forward():

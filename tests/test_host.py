@@ -125,6 +125,44 @@ def test_capi_linear_validation_without_gpu():
     assert call() in (capi.EHIP, capi.EDEVICE)
 
 
+def test_capi_linear_multi_validation_without_gpu():
+    lib = capi.load()
+    fake = 1 << 20
+
+    def projs(n_list, **kw):
+        arr = (capi.Proj * len(n_list))()
+        for i, n in enumerate(n_list):
+            arr[i] = capi.Proj(kw.get("w", fake), kw.get("s", fake), None, kw.get("y", fake),
+                               kw.get("ldy", n), n)
+        return arr
+
+    def call(arr, count, M=1, K=1024, ldx=1024, x=fake, layout=capi.LAYOUT_TILE16X64):
+        return lib.rf_w8a16_linear_multi(x, ldx, layout, arr, count, M, K, 0, None, 0, None)
+
+    ok = projs([4096, 1024, 1024])
+    assert call(ok, 0) == capi.EINVAL
+    assert call(ok, capi.MAX_PROJ + 1) == capi.EINVAL
+    assert call(None, 1) == capi.EINVAL
+    assert call(projs([4096, 0]), 2) == capi.EINVAL
+    assert call(projs([64], ldy=32), 1) == capi.EINVAL
+    assert call(projs([64], w=None), 1) == capi.EINVAL
+    assert call(ok, 3, layout=capi.LAYOUT_ROWMAJOR) == capi.ELAYOUT
+    assert call(projs([64], y=fake + 1), 1) == capi.EALIGN
+    assert call(ok, 3, x=fake + 8) == capi.EALIGN
+    assert call(ok, 3) in (capi.EHIP, capi.EDEVICE)
+
+
+def test_workspace_bytes_multi_matches_single():
+    lib = capi.load()
+    for m, n, k in [(1, 1024, 4096), (16, 4096, 12288), (9, 1000, 1024), (2048, 4096, 4096)]:
+        ns = (ctypes.c_int64 * 1)(n)
+        assert lib.rf_w8a16_workspace_bytes_multi(m, ns, 1, k) == lib.rf_w8a16_workspace_bytes(m, n, k)
+    ns = (ctypes.c_int64 * 3)(4096, 1024, 1024)
+    assert lib.rf_w8a16_workspace_bytes_multi(16, ns, 3, 4096) >= capi.WS_COUNTER_BYTES
+    assert lib.rf_w8a16_workspace_bytes_multi(16, ns, 0, 4096) == 0
+    assert lib.rf_w8a16_workspace_bytes_multi(16, ns, 5, 4096) == 0
+
+
 def test_select_kernel_policy():
     assert rf.select_kernel(1, 4096, 4096) == rf.KERNEL_GEMV
     assert rf.select_kernel(16, 151936, 5120) == rf.KERNEL_GEMV
@@ -144,7 +182,8 @@ def test_workspace_bytes_counter_region():
 
 # ---------------------------------------------------------------- torch op
 def test_torch_op_schemas_registered():
-    for name in ("linear", "linear_into", "pack_weight", "unpack_weight", "select_kernel"):
+    for name in ("linear", "linear_into", "linear_multi", "pack_weight", "unpack_weight",
+                 "select_kernel"):
         assert hasattr(torch.ops.w8a16, name)
 
 
@@ -167,6 +206,8 @@ def test_torch_op_refuses_cpu_tensors():
         rf.linear(x, w, s)
     with pytest.raises(RuntimeError, match="no CPU implementation"):
         rf.linear_into(x, w, s, None, torch.empty(2, 48, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        rf.linear_multi(x, [w, w], [s, s])
 
 
 @pytest.mark.parametrize("bad", ["x_dtype", "w_dtype", "s_dtype", "layout"])
