@@ -113,10 +113,11 @@ typedef struct rf_w8a16_proj {
   int64_t N;
 } rf_w8a16_proj;
 
-/* Workspace bytes rf_w8a16_linear for (M,N,K) with any kernel choice
- * on the current device.  The first RF_W8A16_WS_COUNTER_BYTES bytes are
- * split-K arrival counters: they must be zero before the first call that
- * uses the buffer, and every successful call leaves them zero again. */
+/* Workspace bytes rf_w8a16_linear needs for (M,N,K) with any kernel choice
+ * on the current device (fp32 split-K partials of the GEMV or the GEMM).
+ * The first RF_W8A16_WS_COUNTER_BYTES bytes are split-K arrival counters:
+ * they must be zero before the first call that uses the buffer, and every
+ * successful call leaves them zero again. */
 size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 #define RF_W8A16_WS_COUNTER_BYTES 65536
 
@@ -145,10 +146,10 @@ int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed,
                     void* stream);
 
 /* y_i = x . dequant(w_i)^T (+ b_i) for i < count (1..RF_W8A16_MAX_PROJ),
- * all sharing x [M, ldx] and K (same constraints as rf_w8a16_linear).  With
- * the GEMV (M <= 64) all projections run in ONE launch, so x is read once
- * and the launch ramp is paid once (q/k/v or gate/up of a decoder layer);
- * otherwise one GEMM launch per projection.  Replaces the fused Q/K/V W8A16
+ * all sharing x [M, ldx] and K (same constraints as rf_w8a16_linear).  All
+ * projections run in ONE launch of the chosen kernel (GEMV or GEMM), so the
+ * launch ramp and the last partial round of workgroups are paid once (q/k/v
+ * or gate/up of a decoder layer).  Replaces the fused Q/K/V W8A16
  * launcher `qkv_parallel_w8a16_multibase` (src/ops/rpu_linear.cpp:1546-1674),
  * which runs one launch over three weight and scale bases. */
 int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w8a16_proj* projs,

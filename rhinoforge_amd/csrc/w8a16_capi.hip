@@ -194,17 +194,19 @@ size_t rf_w8a16_workspace_bytes_multi(int64_t M, const int64_t* Ns, int32_t coun
     if (check_nk(Ns[i], K) != RF_W8A16_OK) return 0;
     n32[i] = (int)Ns[i];
   }
-  size_t bytes = RF_W8A16_WS_COUNTER_BYTES;
-  if (M <= 64) {
-    rf::DeviceInfo dev;
-    if (rf::device_info(&dev) != RF_W8A16_OK) {
-      dev.cus = 256;
-      dev.gfx950 = false;
-    }
-    const rf::GemvPlan p = rf::plan_gemv((int)M, n32, count, (int)K, dev);
-    bytes += rf::gemv_workspace_bytes(p, (int)M, n32, count);
+  rf::DeviceInfo dev;
+  if (rf::device_info(&dev) != RF_W8A16_OK) {
+    dev.cus = 256;
+    dev.gfx950 = false;
   }
-  return bytes;
+  // Enough for either kernel family (the caller may force the GEMM at M <= 64).
+  size_t extra = rf::gemm_workspace_bytes(rf::plan_gemm((int)M, n32, count, (int)K, dev));
+  if (M <= 64) {
+    const rf::GemvPlan p = rf::plan_gemv((int)M, n32, count, (int)K, dev);
+    const size_t g = rf::gemv_workspace_bytes(p, (int)M, n32, count);
+    extra = g > extra ? g : extra;
+  }
+  return RF_W8A16_WS_COUNTER_BYTES + extra;
 }
 
 size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
@@ -240,52 +242,39 @@ int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w
   if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
-  if (kernel == RF_W8A16_KERNEL_GEMV) {
-    rf::GemvProblem pr;
-    pr.x = static_cast<const _Float16*>(x);
-    pr.ldx = ldx;
-    pr.M = (int)M;
-    pr.K = (int)K;
-    pr.nproj = count;
-    int n32[RF_W8A16_MAX_PROJ];
-    for (int i = 0; i < count; ++i) {
-      rf::GemvProjection& d = pr.proj[i];
-      d.w = static_cast<const uint8_t*>(projs[i].w_packed);
-      d.scale = static_cast<const _Float16*>(projs[i].scale);
-      d.bias = static_cast<const _Float16*>(projs[i].bias);
-      d.y = static_cast<_Float16*>(projs[i].y);
-      d.ldy = projs[i].ldy;
-      d.N = (int)projs[i].N;
-      n32[i] = d.N;
-    }
-    const rf::GemvPlan p = rf::plan_gemv(pr.M, n32, count, pr.K, dev);
-    if (p.splits > 1) {
-      const size_t need = RF_W8A16_WS_COUNTER_BYTES + rf::gemv_workspace_bytes(p, pr.M, n32, count);
-      if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
-        return RF_W8A16_EWORKSPACE;
-    }
-    const hipError_t e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);
-    return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
-  }
+  rf::LinearProblem pr;
+  pr.x = static_cast<const _Float16*>(x);
+  pr.ldx = ldx;
+  pr.M = (int)M;
+  pr.K = (int)K;
+  pr.nproj = count;
+  int n32[RF_W8A16_MAX_PROJ];
   for (int i = 0; i < count; ++i) {
-    rf::LinearArgs a;
-    a.x = static_cast<const _Float16*>(x);
-    a.ldx = ldx;
-    a.w = static_cast<const uint8_t*>(projs[i].w_packed);
-    a.scale = static_cast<const _Float16*>(projs[i].scale);
-    a.bias = static_cast<const _Float16*>(projs[i].bias);
-    a.y = static_cast<_Float16*>(projs[i].y);
-    a.ldy = projs[i].ldy;
-    a.M = (int)M;
-    a.N = (int)projs[i].N;
-    a.K = (int)K;
-    a.kblocks = (int)ceil_div(K, 64);
-    a.nstrips = (int)ceil_div(a.N, 16);
-    const rf::GemmPlan p = rf::plan_gemm(a.M, a.N, a.K, dev);
-    const hipError_t e = rf::launch_gemm(a, p, s);
-    if (e != hipSuccess) return RF_W8A16_EHIP;
+    rf::Projection& d = pr.proj[i];
+    d.w = static_cast<const uint8_t*>(projs[i].w_packed);
+    d.scale = static_cast<const _Float16*>(projs[i].scale);
+    d.bias = static_cast<const _Float16*>(projs[i].bias);
+    d.y = static_cast<_Float16*>(projs[i].y);
+    d.ldy = projs[i].ldy;
+    d.N = (int)projs[i].N;
+    n32[i] = d.N;
   }
-  return RF_W8A16_OK;
+  auto workspace_ok = [&](size_t extra) {
+    return workspace && workspace_bytes >= RF_W8A16_WS_COUNTER_BYTES + extra &&
+           aligned(workspace, 256);
+  };
+  hipError_t e;
+  if (kernel == RF_W8A16_KERNEL_GEMV) {
+    const rf::GemvPlan p = rf::plan_gemv(pr.M, n32, count, pr.K, dev);
+    if (p.splits > 1 && !workspace_ok(rf::gemv_workspace_bytes(p, pr.M, n32, count)))
+      return RF_W8A16_EWORKSPACE;
+    e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);
+  } else {
+    const rf::GemmPlan p = rf::plan_gemm(pr.M, n32, count, pr.K, dev);
+    if (p.splits > 1 && !workspace_ok(rf::gemm_workspace_bytes(p))) return RF_W8A16_EWORKSPACE;
+    e = rf::launch_gemm(pr, p, p.splits > 1 ? workspace : nullptr, s);
+  }
+  return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
 }
 
 int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed, int32_t layout,

@@ -5,8 +5,8 @@
 // (BM/WAVES_M) x (BN/WAVES_N) block of 16x16 v_mfma_f32_16x16x32_f16
 // accumulators.
 //   * operands move global -> LDS with global_load_lds_dwordx4 (no VGPR
-//     staging), STAGES ring buffers of KS 64-wide K blocks each, so up to
-//     STAGES-1 K steps are in flight while one is multiplied;
+//     staging) into a ring of STAGES 64-wide K blocks, so up to STAGES-1 K
+//     blocks are in flight while one is multiplied;
 //   * A (activations, fp16) rows are 128 bytes per K block, chunk-swizzled
 //     (a_swizzle) so fragment reads are free of LDS bank conflicts;
 //   * B (weights) stays INT8 in LDS (half the LDS bytes and half the
@@ -17,6 +17,13 @@
 //   * tiles are ordered so that the workgroups one XCD runs at the same time
 //     (the hardware deals workgroup ids round-robin over the 8 XCDs) cover a
 //     compact block of output tiles and share A and B rows in their L2;
+//   * one launch can cover up to RF_W8A16_MAX_PROJ weight matrices that
+//     share the activation (q/k/v, gate/up): their tile columns are laid
+//     side by side and each workgroup resolves its matrix from its column;
+//   * when the output has fewer tiles than the chip has workgroup slots, K
+//     is split across workgroups: each split writes its fp32 partial tile to
+//     the workspace and the last split to arrive sums all partials in split
+//     order (deterministic) before the epilogue;
 //   * the per-channel scale and bias are applied in the fp32 epilogue.
 #include "w8a16_common.h"
 #include "w8a16_internal.h"
@@ -25,21 +32,66 @@ namespace rf {
 namespace {
 
 constexpr int kXcds = 8;
+constexpr int kMaxProj = RF_W8A16_MAX_PROJ;
+static_assert(kMaxProj == 4, "target_of selects among exactly four projections");
+
+// One weight matrix of a launch; its tile columns are [tn0, next tn0).
+struct GemmProj {
+  const uint8_t* w;       // TILE16X64 packed
+  const _Float16* scale;  // [N]
+  const _Float16* bias;   // [N] or nullptr
+  _Float16* y;
+  int64_t ldy;
+  int N;
+  int nstrips;
+  int tn0;
+};
 
 struct GemmKernelArgs {
   const _Float16* x;
   int64_t ldx;
+  int M, K;
+  int kblocks;
+  int tiles_m, tiles_n;  // tiles_n summed over the projections
+  int group_m;           // output-tile rows per scheduling group
+  int nproj;
+  GemmProj proj[kMaxProj];
+  int splits;            // K splits (blockIdx.y); 1 = no workspace
+  int kb_per_split;
+  float* partial;        // [splits][tiles][BM*BN], fp32
+  uint32_t* counters;    // [tiles], zero between calls
+};
+
+// The weight matrix (and its tile column) behind global tile column tile_n.
+struct TileTarget {
   const uint8_t* w;
   const _Float16* scale;
   const _Float16* bias;
   _Float16* y;
   int64_t ldy;
-  int M, N, K;
-  int kblocks;
+  int N;
   int nstrips;
-  int tiles_m, tiles_n;
-  int group_m;  // output-tile rows per scheduling group
+  int tn;
 };
+
+__device__ __forceinline__ TileTarget target_of(const GemmKernelArgs& a, int tile_n) {
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProj; ++i) p = (i < a.nproj && tile_n >= a.proj[i].tn0) ? i : p;
+  // Selects, not an indexed load: the argument block stays in SGPRs.
+#define RF_PICK(f) (p == 0 ? a.proj[0].f : p == 1 ? a.proj[1].f : p == 2 ? a.proj[2].f : a.proj[3].f)
+  TileTarget t;
+  t.w = RF_PICK(w);
+  t.scale = RF_PICK(scale);
+  t.bias = RF_PICK(bias);
+  t.y = RF_PICK(y);
+  t.ldy = RF_PICK(ldy);
+  t.N = RF_PICK(N);
+  t.nstrips = RF_PICK(nstrips);
+  t.tn = tile_n - RF_PICK(tn0);
+#undef RF_PICK
+  return t;
+}
 
 // Workgroup id -> (tile_m, tile_n).  Ids are first regrouped so that the
 // ids one XCD receives (id % 8 == x) form one contiguous run of tile
@@ -59,28 +111,26 @@ __device__ __forceinline__ void tile_of(int bid, const GemmKernelArgs& a, int& t
   tn = r / gm;
 }
 
-// ---------------------------------------------------------------------------
-// Direct-to-LDS variant: global_load_lds_dwordx4 writes each wavefront's
-// 64 x 16 bytes straight into LDS (lane-contiguous), so no VGPRs stage the
-// tiles and STAGES K steps can be in flight.  A rows are unpadded (128 B)
-// and chunk-swizzled instead (a_swizzle): LDS slot p of row r holds global
-// chunk p ^ a_swizzle(r).  Rows past M and strips past N load clamped (valid)
-// addresses; their results are never stored.  Columns past K (the last K
-// step when K % 64 != 0) are zeroed in LDS after their load lands.
-// ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 // One global_load_lds_dwordx4: every lane reads 16 bytes at `g`, the
 // wavefront's 64 x 16 bytes land lane-contiguously at LDS byte address
 // `lds` (wave-uniform, passed in M0).  Written as inline asm so the
 // compiler does not serialise every later LDS read behind it (it cannot
-// tell which LDS bytes a DMA writes); the kernel orders the LDS traffic
-// itself with explicit s_waitcnt vmcnt + s_barrier.  Nothing else in these
-// kernels uses M0.
+// tell which LDS bytes a DMA writes); the kernels order the LDS traffic
+// themselves with explicit s_waitcnt vmcnt + s_barrier.  Nothing else in
+// these kernels uses M0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
+}
+
+// The same with a wave-uniform SGPR base and a per-lane 32-bit byte offset
+// (global_load_lds_dwordx4 voff, s[base]).
+__device__ __forceinline__ void dma16s(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -101,186 +151,67 @@ __device__ __forceinline__ void barrier_lds() {
   __asm__ volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int KS>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(GemmKernelArgs a) {
-  constexpr int NT = WAVES_M * WAVES_N * 64;
-  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int A_KB = BM * 128;                  // A bytes of one 64-wide K block
-  constexpr int B_TILES = BN / 16;
-  constexpr int B_KB = B_TILES * kTileBytes;      // B bytes of one K block
-  constexpr int A_BYTES = A_KB * KS, B_BYTES = B_KB * KS;
-  constexpr int STAGE = A_BYTES + B_BYTES;        // KS K blocks per stage
-  constexpr int A_LOADS = A_BYTES / (NT * 16);    // per thread per stage
-  constexpr int B_LOADS = B_BYTES / (NT * 16);
-  constexpr int ROWBLKS = BM / 8;                 // 1 KB (8-row) blocks per A K block
-  static_assert(A_LOADS >= 1 && B_LOADS >= 1 && A_LOADS * NT * 16 == A_BYTES &&
-                    B_LOADS * NT * 16 == B_BYTES,
-                "tile does not split into whole 1 KB wavefront loads");
-  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
-  static_assert(TM >= 1 && TN >= 1, "wavefront tile");
+// Buffer resource over the split-K partials; accesses use sc1 (device-scope
+// coherent: written through / re-fetched past the issuing XCD's L2, the
+// same instructions as relaxed agent-scope atomic stores and loads).
+// 0x00020000: raw 32-bit data format word of CDNA buffer descriptors.
+constexpr int kCoherent = 16;  // cache-policy bit sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
+}
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  int tile_m, tile_n;
-  tile_of(blockIdx.x, a, tile_m, tile_n);
-  const int m0 = tile_m * BM;
-  const int strip0 = tile_n * B_TILES;
-  const int nk = a.kblocks;
-  const int nstage = (nk + KS - 1) / KS;
-
-  // A load i of this thread: 1 KB block j = wave*A_LOADS + i of the stage,
-  // K block kk = j / ROWBLKS, LDS slot p = (j % ROWBLKS)*64 + lane, row
-  // p/8, global chunk (p%8) ^ ((row>>1)&7).
-  const _Float16* asrc[A_LOADS];
-  int acol[A_LOADS];  // column offset inside the stage's KS*64 columns
-#pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) {
-    const int j = wave * A_LOADS + i;
-    const int kk = j / ROWBLKS;
-    const int p = (j % ROWBLKS) * 64 + lane;
-    const int row = p >> 3;
-    const int chunk = (p & 7) ^ a_swizzle(row);
-    acol[i] = kk * 64 + chunk * 8;
-    const int m = min(m0 + row, a.M - 1);
-    asrc[i] = a.x + (int64_t)m * a.ldx + acol[i];
-  }
-  // B load i: 1 KB block j = K block kk = j / B_TILES, tile t = j % B_TILES.
-  const uint8_t* bsrc[B_LOADS];
-  int bkk[B_LOADS];
-#pragma unroll
-  for (int i = 0; i < B_LOADS; ++i) {
-    const int j = wave * B_LOADS + i;
-    bkk[i] = j / B_TILES;
-    const int strip = min(strip0 + j % B_TILES, a.nstrips - 1);
-    bsrc[i] = a.w + (int64_t)strip * a.kblocks * kTileBytes + lane * 16;
-  }
-  const bool k_tail = (a.K & 63) != 0 || (nk % KS) != 0;
-
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)smem;
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  auto issue = [&](int st_idx) {
-    const uint32_t st = lds0 + (st_idx % STAGES) * STAGE;
-    const int kcol = st_idx * KS * 64;
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      // Columns past K would read past the row: load column 0 instead and
-      // zero the slot once it has landed (fix_tail).
-      const _Float16* src = kcol + acol[i] < a.K ? asrc[i] + kcol : asrc[i] - acol[i];
-      dma16(src, st + (wave_u * A_LOADS + i) * 1024);
-    }
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      // K blocks past the weight's last one are clamped; A is zero there.
-      const int kb = min(st_idx * KS + bkk[i], nk - 1);
-      dma16(bsrc[i] + (int64_t)kb * kTileBytes, st + A_BYTES + (wave_u * B_LOADS + i) * 1024);
-    }
-  };
-  auto fix_tail = [&](int st_idx) {
-    uint8_t* st = smem + (st_idx % STAGES) * STAGE;
-    const int kcol = st_idx * KS * 64;
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i)
-      if (kcol + acol[i] >= a.K)
-        *reinterpret_cast<uint4*>(st + (wave * A_LOADS + i) * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
-  };
-
-  floatx4 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  const int arow = wm * WM + (lane & 15);
-  const int sw = a_swizzle(arow);  // same for arow + 16*i
-  const int aoff0 = arow * 128 + (((2 * (lane >> 4)) ^ sw) * 16);
-  const int aoff1 = arow * 128 + (((2 * (lane >> 4) + 1) ^ sw) * 16);
-
-  auto compute = [&](int st_idx) {
-    const uint8_t* st = smem + (st_idx % STAGES) * STAGE;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      const uint8_t* sa = st + kk * A_KB;
-      const uint8_t* sb = st + A_BYTES + kk * B_KB;
-      uint4 braw[TN];
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        braw[j] = *reinterpret_cast<const uint4*>(sb + (wn * TN + j) * kTileBytes + lane * 16);
-#pragma unroll
-      for (int step = 0; step < 2; ++step) {
-        half8 af[TM], bf[TN];
-        const int aoff = step == 0 ? aoff0 : aoff1;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-          af[i] = *reinterpret_cast<const half8*>(sa + aoff + i * 16 * 128);
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          bf[j] = step == 0 ? dequant8(braw[j].x, braw[j].y) : dequant8(braw[j].z, braw[j].w);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
-      }
-    }
-  };
-
-  // Prologue: STAGES-1 stages in flight.
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < nstage) issue(s);
-  for (int sidx = 0; sidx < nstage; ++sidx) {
-    // Wait for this thread's loads of stage sidx (later stages may stay in
-    // flight), then for everyone's.
-    const int ahead = min(STAGES - 2, nstage - 1 - sidx);  // stages issued after sidx
-    if (ahead >= 2) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (A_LOADS + B_LOADS)) : "memory");
-    else if (ahead == 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(A_LOADS + B_LOADS) : "memory");
-    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (k_tail && sidx == nstage - 1) fix_tail(sidx);
-    barrier_lds();
-    // Everyone is past compute(sidx-1): its stage can be refilled.
-    if (sidx + STAGES - 1 < nstage) issue(sidx + STAGES - 1);
-    compute(sidx);
-  }
-
-  // Epilogue: lane l holds D[4*(l/16) + r][l%16] of each 16x16 tile.
+// fp32 epilogue: y = acc * scale[n] + bias[n].  Lane l holds
+// D[4*(l/16) + r][l%16] of each 16x16 tile; a full tile stores without
+// per-element checks.
+template <int TM, int TN>
+__device__ __forceinline__ void store_tile(const TileTarget& t, const floatx4 (&acc)[TM][TN],
+                                           int m0w, int n0w, int lane, int M, bool full) {
+  const int nl = n0w + (lane & 15);
+  const int ml = m0w + 4 * (lane >> 4);
+  _Float16* yl = t.y + (int64_t)ml * t.ldy + nl;
+  float sc[TN], bi[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int n = (strip0 + wn * TN + j) * 16 + (lane & 15);
-    if (n >= a.N) continue;
-    const float sc = (float)a.scale[n];
-    const float bi = a.bias ? (float)a.bias[n] : 0.f;
+    const int n = nl + j * 16;
+    sc[j] = n < t.N ? (float)t.scale[n] : 0.f;
+    bi[j] = (t.bias && n < t.N) ? (float)t.bias[n] : 0.f;
+  }
+  if (full) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
-        if (m < a.M) a.y[(int64_t)m * a.ldy + n] = (_Float16)__builtin_fmaf(acc[i][j][r], sc, bi);
+        _Float16* yr = yl + (int64_t)(i * 16 + r) * t.ldy;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) yr[j * 16] = (_Float16)__builtin_fmaf(acc[i][j][r], sc[j], bi[j]);
       }
-    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (ml + i * 16 + r >= M) continue;
+        _Float16* yr = yl + (int64_t)(i * 16 + r) * t.ldy;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          if (nl + j * 16 < t.N) yr[j * 16] = (_Float16)__builtin_fmaf(acc[i][j][r], sc[j], bi[j]);
+      }
   }
 }
 
 // ---------------------------------------------------------------------------
-// v3: the DMA kernel with wave-uniform SGPR bases.  Each DMA is
-// global_load_lds_dwordx4 voff, s[base]: the per-lane byte offset from the
-// tile's first row / strip is fixed for the whole K loop, and one scalar add
-// per K block moves the bases, so the loop issues no vector address math.
-// OCC workgroups per CU are requested from the register allocator.
-// Offsets are 32-bit: the host checks BM*ldx*2 + 2K and the strip span
-// B_TILES*kblocks*1024 fit (launch_v3_t).
+// Main kernel.  Each DMA is global_load_lds_dwordx4 voff, s[base]: the
+// per-lane byte offset from the tile's first row / strip is fixed for the
+// whole K loop, and one scalar add per K block moves the bases, so the loop
+// issues no vector address math.  OCC workgroups per CU are requested from
+// the register allocator.  Offsets are 32-bit: the host checks that
+// BM*ldx*2 + 2K and the strip span of BN/16 strips fit (v3_offsets_fit).
+//
+// LDS A rows are unpadded (128 B) and chunk-swizzled: slot p of row r holds
+// global chunk p ^ a_swizzle(r).  Rows past M and strips past N load clamped
+// (valid) addresses; their results are never stored.  Columns past K (the
+// last K block when K % 64 != 0) are zeroed in LDS after their load lands.
 // ---------------------------------------------------------------------------
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16s(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(OCC * WAVES_M * WAVES_N / 4, 8)))
 void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
@@ -305,15 +236,19 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int tile = blockIdx.x;
+  const int split = blockIdx.y;
   int tile_m, tile_n;
-  tile_of(blockIdx.x, a, tile_m, tile_n);
+  tile_of(tile, a, tile_m, tile_n);
+  const TileTarget tt = target_of(a, tile_n);
   const int m0 = tile_m * BM;
-  const int strip0 = tile_n * B_TILES;
-  const int nk = a.kblocks;
+  const int strip0 = tt.tn * B_TILES;
+  const int kb0 = split * a.kb_per_split;
+  const int nk = min(a.kblocks - kb0, a.kb_per_split);  // K blocks of this split (>= 1)
 
   // Wave-uniform bases and per-lane 32-bit offsets.
   const uint8_t* abase = reinterpret_cast<const uint8_t*>(a.x + (int64_t)m0 * a.ldx);
-  const uint8_t* bbase = a.w + (int64_t)strip0 * a.kblocks * kTileBytes;
+  const uint8_t* bbase = tt.w + (int64_t)strip0 * a.kblocks * kTileBytes;
   uint32_t aoff[A_LOADS], arow_off[A_LOADS];
   int acol[A_LOADS];
 #pragma unroll
@@ -329,8 +264,204 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   uint32_t boff[B_LOADS];
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
-    const int t = min(strip0 + wave * B_LOADS + i, a.nstrips - 1) - strip0;
+    const int t = min(strip0 + wave * B_LOADS + i, tt.nstrips - 1) - strip0;
     boff[i] = (uint32_t)t * (uint32_t)a.kblocks * kTileBytes + lane * 16;
+  }
+  const bool k_tail = (a.K & 63) != 0;
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)smem;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // Local K block i of this split = global K block kb0 + i, LDS stage i % STAGES.
+  auto issue = [&](int i) {
+    const int kb = kb0 + i;
+    const uint32_t st = lds0 + (i % STAGES) * STAGE;
+    if (k_tail && kb == a.kblocks - 1) {
+      // Last block with columns past K: those chunks load column 0 instead
+      // and are zeroed after they land (fix_tail).
+#pragma unroll
+      for (int l = 0; l < A_LOADS; ++l) {
+        const uint32_t o = kb * 64 + acol[l] < a.K ? aoff[l] + kb * 128 : arow_off[l];
+        dma16s(o, abase, st + (wave_u * A_LOADS + l) * 1024);
+      }
+    } else {
+      const uint8_t* ab = abase + kb * 128;
+#pragma unroll
+      for (int l = 0; l < A_LOADS; ++l) dma16s(aoff[l], ab, st + (wave_u * A_LOADS + l) * 1024);
+    }
+    const uint8_t* bb = bbase + (int64_t)kb * kTileBytes;
+#pragma unroll
+    for (int l = 0; l < B_LOADS; ++l) dma16s(boff[l], bb, st + A_BYTES + (wave_u * B_LOADS + l) * 1024);
+  };
+  auto fix_tail = [&](int i) {
+    const int kb = kb0 + i;
+    uint8_t* st = smem + (i % STAGES) * STAGE;
+#pragma unroll
+    for (int l = 0; l < A_LOADS; ++l)
+      if (kb * 64 + acol[l] >= a.K)
+        *reinterpret_cast<uint4*>(st + (wave * A_LOADS + l) * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
+  };
+
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int arow = wm * WM + (lane & 15);
+  const int sw = a_swizzle(arow);  // same for arow + 16*i
+  const int aoff0 = arow * 128 + (((2 * (lane >> 4)) ^ sw) * 16);
+  const int aoff1 = arow * 128 + (((2 * (lane >> 4) + 1) ^ sw) * 16);
+  auto compute = [&](int i) {
+    const uint8_t* st = smem + (i % STAGES) * STAGE;
+    uint4 braw[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      braw[j] = *reinterpret_cast<const uint4*>(st + A_BYTES + (wn * TN + j) * kTileBytes + lane * 16);
+#pragma unroll
+    for (int step = 0; step < 2; ++step) {
+      half8 af[TM];
+      const int ao = step == 0 ? aoff0 : aoff1;
+#pragma unroll
+      for (int r = 0; r < TM; ++r) af[r] = *reinterpret_cast<const half8*>(st + ao + r * 16 * 128);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const half8 b = step == 0 ? dequant8(braw[j].x, braw[j].y) : dequant8(braw[j].z, braw[j].w);
+#pragma unroll
+        for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(af[r], b, acc[r][j]);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nk) issue(s);
+  for (int i = 0; i < nk; ++i) {
+    const int ahead = min(STAGES - 2, nk - 1 - i);  // blocks issued after i
+    if (ahead >= 2) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LOADS) : "memory");
+    else if (ahead == 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS) : "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (k_tail && kb0 + i == a.kblocks - 1) fix_tail(i);
+    barrier_lds();
+    // Everyone is past compute(i-1): its stage can be refilled.
+    if (i + STAGES - 1 < nk) issue(i + STAGES - 1);
+    compute(i);
+  }
+
+  if (a.splits > 1) {
+    // Partial tile in lane order: element (wave, i, j, r) of lane l at
+    // ((((wave*TM + i)*TN + j)*4 + r)*64 + l) floats, so every store and
+    // load below moves 256 contiguous bytes per wavefront.
+    constexpr uint32_t TILE_F = BM * BN;
+    const int tiles = a.tiles_m * a.tiles_n;
+    const __amdgpu_buffer_rsrc_t pr =
+        partial_rsrc(a.partial, (uint32_t)((uint64_t)a.splits * tiles * TILE_F * 4));
+    const uint32_t own = ((uint32_t)split * tiles + tile) * TILE_F * 4;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t off = ((((wave * TM + i) * TN + j) * 4 + r) * 64 + lane) * 4;
+          // Copy the element out first: a bit cast of the vector-element
+          // lvalue itself reads element 0 whatever r is.
+          const float v = acc[i][j][r];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pr, own + off, 0,
+                                                kCoherent);
+        }
+    __shared__ uint32_t is_last;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores landed
+    barrier_lds();
+    if (tid == 0) {
+      const uint32_t prev =
+          __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = prev == (uint32_t)(a.splits - 1) ? 1u : 0u;
+    }
+    barrier_lds();
+    if (!is_last) return;
+    // Last to arrive: sum every split's partial (its own included, read
+    // back) in split order, so the result does not depend on arrival order.
+    for (int sp = 0; sp < a.splits; ++sp) {
+      const uint32_t base = ((uint32_t)sp * tiles + tile) * TILE_F * 4;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t off = ((((wave * TM + i) * TN + j) * 4 + r) * 64 + lane) * 4;
+            const float v = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(pr, base + off, 0, kCoherent));
+            acc[i][j][r] = sp == 0 ? v : acc[i][j][r] + v;
+          }
+    }
+    if (tid == 0)
+      __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  const bool full = m0 + BM <= a.M && (strip0 + B_TILES) * 16 <= tt.N;
+  store_tile<TM, TN>(tt, acc, m0 + wm * WM, (strip0 + wn * TN) * 16, lane, a.M, full);
+}
+
+// True when the 32-bit DMA offsets of w8a16_gemm_v3_kernel cannot overflow
+// for any projection of the launch.
+inline bool v3_offsets_fit(const GemmKernelArgs& ka, int bm, int bn) {
+  const uint64_t a_span = (uint64_t)bm * (uint64_t)ka.ldx * 2 + (uint64_t)ka.kblocks * 128;
+  const uint64_t b_span = (uint64_t)(bn / 16) * (uint64_t)ka.kblocks * kTileBytes;
+  return a_span < (1ull << 32) && b_span < (1ull << 32);
+}
+
+// ---------------------------------------------------------------------------
+// 64-bit fallback: the same pipeline with full per-lane addresses, for
+// shapes whose 32-bit tile offsets could overflow (huge ldx or K).  One K
+// range (no split).
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(GemmKernelArgs a) {
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int A_BYTES = BM * 128;
+  constexpr int B_TILES = BN / 16;
+  constexpr int B_BYTES = B_TILES * kTileBytes;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int A_LOADS = A_BYTES / (NT * 16);
+  constexpr int B_LOADS = B_BYTES / (NT * 16);
+  constexpr int LOADS = A_LOADS + B_LOADS;
+  static_assert(A_LOADS >= 1 && B_LOADS >= 1 && A_LOADS * NT * 16 == A_BYTES &&
+                    B_LOADS * NT * 16 == B_BYTES,
+                "tile does not split into whole 1 KB wavefront loads");
+  static_assert(STAGES >= 2 && STAGES <= 3, "2..3 stages");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  int tile_m, tile_n;
+  tile_of(blockIdx.x, a, tile_m, tile_n);
+  const TileTarget tt = target_of(a, tile_n);
+  const int m0 = tile_m * BM;
+  const int strip0 = tt.tn * B_TILES;
+  const int nk = a.kblocks;
+
+  const _Float16* asrc[A_LOADS];
+  int acol[A_LOADS];
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i) {
+    const int p = (wave * A_LOADS + i) * 64 + lane;
+    const int row = p >> 3;
+    const int chunk = (p & 7) ^ a_swizzle(row);
+    acol[i] = chunk * 8;
+    const int m = min(m0 + row, a.M - 1);
+    asrc[i] = a.x + (int64_t)m * a.ldx + acol[i];
+  }
+  const uint8_t* bsrc[B_LOADS];
+#pragma unroll
+  for (int i = 0; i < B_LOADS; ++i) {
+    const int strip = min(strip0 + wave * B_LOADS + i, tt.nstrips - 1);
+    bsrc[i] = tt.w + (int64_t)strip * a.kblocks * kTileBytes + lane * 16;
   }
   const bool k_tail = (a.K & 63) != 0;
 
@@ -338,22 +469,14 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   auto issue = [&](int kb) {
     const uint32_t st = lds0 + (kb % STAGES) * STAGE;
-    if (k_tail && kb == nk - 1) {
-      // Last block with columns past K: those chunks load column 0 instead
-      // and are zeroed after they land (fix_tail).
 #pragma unroll
-      for (int i = 0; i < A_LOADS; ++i) {
-        const uint32_t o = kb * 64 + acol[i] < a.K ? aoff[i] + kb * 128 : arow_off[i];
-        dma16s(o, abase, st + (wave_u * A_LOADS + i) * 1024);
-      }
-    } else {
-      const uint8_t* ab = abase + kb * 128;
-#pragma unroll
-      for (int i = 0; i < A_LOADS; ++i) dma16s(aoff[i], ab, st + (wave_u * A_LOADS + i) * 1024);
+    for (int i = 0; i < A_LOADS; ++i) {
+      const _Float16* src = kb * 64 + acol[i] < a.K ? asrc[i] + kb * 64 : asrc[i] - acol[i];
+      dma16(src, st + (wave_u * A_LOADS + i) * 1024);
     }
-    const uint8_t* bb = bbase + (int64_t)kb * kTileBytes;
 #pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) dma16s(boff[i], bb, st + A_BYTES + (wave_u * B_LOADS + i) * 1024);
+    for (int i = 0; i < B_LOADS; ++i)
+      dma16(bsrc[i] + (int64_t)kb * kTileBytes, st + A_BYTES + (wave_u * B_LOADS + i) * 1024);
   };
   auto fix_tail = [&](int kb) {
     uint8_t* st = smem + (kb % STAGES) * STAGE;
@@ -370,7 +493,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int arow = wm * WM + (lane & 15);
-  const int sw = a_swizzle(arow);  // same for arow + 16*i
+  const int sw = a_swizzle(arow);
   const int aoff0 = arow * 128 + (((2 * (lane >> 4)) ^ sw) * 16);
   const int aoff1 = arow * 128 + (((2 * (lane >> 4) + 1) ^ sw) * 16);
   auto compute = [&](int kb) {
@@ -384,12 +507,12 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
       half8 af[TM];
       const int ao = step == 0 ? aoff0 : aoff1;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const half8*>(st + ao + i * 16 * 128);
+      for (int r = 0; r < TM; ++r) af[r] = *reinterpret_cast<const half8*>(st + ao + r * 16 * 128);
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const half8 b = step == 0 ? dequant8(braw[j].x, braw[j].y) : dequant8(braw[j].z, braw[j].w);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) acc[i][j] = mfma16x16x32(af[i], b, acc[i][j]);
+        for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(af[r], b, acc[r][j]);
       }
     }
   };
@@ -398,9 +521,8 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < nk) issue(s);
   for (int kb = 0; kb < nk; ++kb) {
-    const int ahead = min(STAGES - 2, nk - 1 - kb);  // blocks issued after kb
-    if (ahead >= 2) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LOADS) : "memory");
-    else if (ahead == 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS) : "memory");
+    const int ahead = min(STAGES - 2, nk - 1 - kb);
+    if (ahead >= 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS) : "memory");
     else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (k_tail && kb == nk - 1) fix_tail(kb);
     barrier_lds();
@@ -408,85 +530,29 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     compute(kb);
   }
 
-  // Epilogue: lane l holds D[4*(l/16) + r][l%16] of each 16x16 tile; row
-  // offsets are uniform, so a full tile stores without per-element checks.
-  const int nl = (strip0 + wn * TN) * 16 + (lane & 15);
-  const int ml = m0 + wm * WM + 4 * (lane >> 4);
-  _Float16* yl = a.y + (int64_t)ml * a.ldy + nl;
-  float sc[TN], bi[TN];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = nl + j * 16;
-    sc[j] = n < a.N ? (float)a.scale[n] : 0.f;
-    bi[j] = (a.bias && n < a.N) ? (float)a.bias[n] : 0.f;
-  }
-  const bool full = m0 + BM <= a.M && (strip0 + B_TILES) * 16 <= a.N;
-  if (full) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        _Float16* yr = yl + (int64_t)(i * 16 + r) * a.ldy;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) yr[j * 16] = (_Float16)__builtin_fmaf(acc[i][j][r], sc[j], bi[j]);
-      }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (ml + i * 16 + r >= a.M) continue;
-        _Float16* yr = yl + (int64_t)(i * 16 + r) * a.ldy;
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          if (nl + j * 16 < a.N) yr[j * 16] = (_Float16)__builtin_fmaf(acc[i][j][r], sc[j], bi[j]);
-      }
-  }
-}
-
-// True when the 32-bit DMA offsets of w8a16_gemm_v3_kernel cannot overflow.
-inline bool v3_offsets_fit(const GemmKernelArgs& ka, int bm, int bn) {
-  const uint64_t a_span = (uint64_t)bm * (uint64_t)ka.ldx * 2 + (uint64_t)ka.kblocks * 128;
-  const uint64_t b_span = (uint64_t)(bn / 16) * (uint64_t)ka.kblocks * kTileBytes;
-  return a_span < (1ull << 32) && b_span < (1ull << 32);
+  const bool full = m0 + BM <= a.M && (strip0 + B_TILES) * 16 <= tt.N;
+  store_tile<TM, TN>(tt, acc, m0 + wm * WM, (strip0 + wn * TN) * 16, lane, a.M, full);
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
 hipError_t launch_v3_t(const GemmKernelArgs& ka, hipStream_t stream) {
-  const int64_t blocks = (int64_t)ka.tiles_m * ka.tiles_n;
-  if (blocks <= 0 || blocks > 0x7fffffff || !v3_offsets_fit(ka, BM, BN)) return hipErrorInvalidValue;
+  const int64_t tiles = (int64_t)ka.tiles_m * ka.tiles_n;
+  if (tiles <= 0 || tiles > 0x7fffffff || ka.splits < 1 || ka.splits > 65535 ||
+      !v3_offsets_fit(ka, BM, BN))
+    return hipErrorInvalidValue;
   hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC>),
-                     dim3((unsigned)blocks), dim3(WAVES_M * WAVES_N * 64), 0, stream, ka);
+                     dim3((unsigned)tiles, (unsigned)ka.splits), dim3(WAVES_M * WAVES_N * 64), 0,
+                     stream, ka);
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int KS>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES>
 hipError_t launch_dma_t(const GemmKernelArgs& ka, hipStream_t stream) {
-  const int64_t blocks = (int64_t)ka.tiles_m * ka.tiles_n;
-  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((w8a16_gemm_dma_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, KS>),
-                     dim3((unsigned)blocks), dim3(WAVES_M * WAVES_N * 64), 0, stream, ka);
+  const int64_t tiles = (int64_t)ka.tiles_m * ka.tiles_n;
+  if (tiles <= 0 || tiles > 0x7fffffff || ka.splits != 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((w8a16_gemm_dma_kernel<BM, BN, WAVES_M, WAVES_N, STAGES>),
+                     dim3((unsigned)tiles), dim3(WAVES_M * WAVES_N * 64), 0, stream, ka);
   return hipGetLastError();
-}
-
-GemmKernelArgs make_args(const LinearArgs& a, const GemmPlan& p) {
-  GemmKernelArgs ka;
-  ka.x = a.x;
-  ka.ldx = a.ldx;
-  ka.w = a.w;
-  ka.scale = a.scale;
-  ka.bias = a.bias;
-  ka.y = a.y;
-  ka.ldy = a.ldy;
-  ka.M = a.M;
-  ka.N = a.N;
-  ka.K = a.K;
-  ka.kblocks = a.kblocks;
-  ka.nstrips = a.nstrips;
-  ka.tiles_m = p.tiles_m;
-  ka.tiles_n = p.tiles_n;
-  ka.group_m = p.group_m;
-  return ka;
 }
 
 }  // namespace
@@ -497,54 +563,147 @@ enum GemmCfgId {
   kV3M128N128,    // 4 wavefronts 1x4, 2 stages, 3 workgroups/CU: M >= 1024, N < 8192
   kV3M128N128S3,  // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: moderate M and N
   kV3M64N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: small M
+  kV3M256N256,    // 8 wavefronts 2x4, 2 stages, 1 workgroup/CU: whole rounds of big tiles
   kDmaM128N128,   // 64-bit addresses: when the v3 32-bit offsets could overflow
   kGemmCfgCount
 };
 
-constexpr int kGemmTile[kGemmCfgCount][2] = {{128, 256}, {128, 128}, {128, 128}, {64, 256}, {128, 128}};
+// {BM, BN, workgroups per CU}
+constexpr int kGemmTile[kGemmCfgCount][3] = {{128, 256, 2}, {128, 128, 3}, {128, 128, 2},
+                                             {64, 256, 2},  {256, 256, 1}, {128, 128, 1}};
+
+namespace {
+
+constexpr int kMaxGemmSplits = 8;
+constexpr int kMinKbPerSplit = 16;  // 1024 input channels per split at least
+constexpr int kMaxSplitTiles = RF_W8A16_WS_COUNTER_BYTES / 4;
+
+void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
+  p.bm = kGemmTile[p.cfg][0];
+  p.bn = kGemmTile[p.cfg][1];
+  p.tiles_m = (int)ceil_div(M, p.bm);
+  p.tiles_n = 0;
+  for (int i = 0; i < nproj; ++i) p.tiles_n += (int)ceil_div(Ns[i], p.bn);
+  p.group_m = p.tiles_m < 4 ? p.tiles_m : 4;
+}
+
+}  // namespace
 
 // Kernel choice per shape: the analogue of the reference's W8A16 tile
 // tables (src/ops/rpu_linear_tiling.h:69-127, selectors :544-595), as rules
-// over (M, N) tuned on MI355X.
-GemmPlan plan_gemm(int M, int N, int /*K*/, const DeviceInfo& /*dev*/) {
-  GemmPlan p;
-  int cfg;
-  if (M < 128) {
-    cfg = kV3M64N256;
-  } else if (M >= 1024) {
-    cfg = N >= 8192 ? kV3M128N256 : kV3M128N128;
-  } else {
-    cfg = N >= 16384 ? kV3M128N256 : kV3M128N128S3;
+// over (M, total N) tuned on MI355X, plus a K split when the output has
+// fewer tiles than the chip has workgroup slots.
+GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev) {
+  const int cus = dev.cus > 0 ? dev.cus : 256;
+  int64_t ntotal = 0, t256 = 0;
+  for (int i = 0; i < nproj; ++i) {
+    ntotal += Ns[i];
+    t256 += ceil_div(Ns[i], 256);
   }
-  p.cfg = cfg;
-  p.bm = kGemmTile[cfg][0];
-  p.bn = kGemmTile[cfg][1];
-  p.tiles_m = (int)ceil_div(M, p.bm);
-  p.tiles_n = (int)ceil_div(N, p.bn);
-  p.group_m = p.tiles_m < 4 ? p.tiles_m : 4;
+  t256 *= ceil_div(M, 256);
+  GemmPlan p;
+  if (M < 128) {
+    p.cfg = kV3M64N256;
+  } else if (M >= 1024) {
+    // 256x256 tiles only when they fill whole rounds of the chip (or many
+    // rounds): at 1.5 rounds the half-empty last round costs more than the
+    // bigger tile gains.
+    if (t256 % cus == 0 || t256 >= 4 * cus) p.cfg = kV3M256N256;
+    else p.cfg = ntotal >= 8192 ? kV3M128N256 : kV3M128N128;
+  } else {
+    p.cfg = ntotal >= 16384 ? kV3M128N256 : kV3M128N128S3;
+  }
+  set_tiles(p, M, Ns, nproj);
+  const int kblocks = (int)ceil_div(K, 64);
+  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+  const int64_t slots = (int64_t)cus * kGemmTile[p.cfg][2];
+  p.splits = 1;
+  p.kb_per_split = kblocks;
+  if (tiles < slots && tiles <= kMaxSplitTiles) {
+    int s = (int)(slots / tiles);
+    s = s < kMaxGemmSplits ? s : kMaxGemmSplits;
+    s = s < kblocks / kMinKbPerSplit ? s : kblocks / kMinKbPerSplit;
+    if (s >= 2) {
+      p.kb_per_split = (int)ceil_div(kblocks, s);
+      p.splits = (int)ceil_div(kblocks, p.kb_per_split);  // no empty split
+    }
+  }
   return p;
 }
 
-hipError_t launch_gemm(const LinearArgs& a, const GemmPlan& plan, hipStream_t stream) {
+size_t gemm_workspace_bytes(const GemmPlan& p) {
+  if (p.splits <= 1) return 0;
+  return (size_t)p.splits * (size_t)p.tiles_m * (size_t)p.tiles_n * (size_t)p.bm * (size_t)p.bn *
+         sizeof(float);
+}
+
+hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* workspace,
+                       hipStream_t stream) {
   GemmPlan p = plan;
-  GemmKernelArgs ka = make_args(a, p);
+  if (pr.nproj < 1 || pr.nproj > kMaxProj) return hipErrorInvalidValue;
+  int ns[kMaxProj];
+  for (int i = 0; i < pr.nproj; ++i) ns[i] = pr.proj[i].N;
+
+  GemmKernelArgs ka;
+  ka.x = pr.x;
+  ka.ldx = pr.ldx;
+  ka.M = pr.M;
+  ka.K = pr.K;
+  ka.kblocks = (int)ceil_div(pr.K, 64);
+  ka.nproj = pr.nproj;
+  auto fill = [&](const GemmPlan& q) {
+    ka.tiles_m = q.tiles_m;
+    ka.tiles_n = q.tiles_n;
+    ka.group_m = q.group_m;
+    int tn0 = 0;
+    for (int i = 0; i < kMaxProj; ++i) {
+      GemmProj& d = ka.proj[i];
+      if (i < pr.nproj) {
+        const Projection& s = pr.proj[i];
+        d.w = s.w;
+        d.scale = s.scale;
+        d.bias = s.bias;
+        d.y = s.y;
+        d.ldy = s.ldy;
+        d.N = s.N;
+        d.nstrips = (int)ceil_div(s.N, 16);
+        d.tn0 = tn0;
+        tn0 += (int)ceil_div(s.N, q.bn);
+      } else {
+        d = ka.proj[0];
+        d.tn0 = 0x7fffffff;
+      }
+    }
+    ka.splits = q.splits;
+    ka.kb_per_split = q.kb_per_split;
+    ka.partial = nullptr;
+    ka.counters = nullptr;
+    if (q.splits > 1) {
+      ka.counters = static_cast<uint32_t*>(workspace);
+      ka.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + RF_W8A16_WS_COUNTER_BYTES);
+    }
+  };
+  fill(p);
   // The v3 kernels address a tile with 32-bit offsets from its first row /
   // strip (row stride ldx); fall back to 64-bit addressing when those could
   // overflow.
   if (p.cfg != kDmaM128N128 && !v3_offsets_fit(ka, p.bm, p.bn)) {
     p.cfg = kDmaM128N128;
-    p.bm = p.bn = 128;
-    p.tiles_m = (int)ceil_div(a.M, 128);
-    p.tiles_n = (int)ceil_div(a.N, 128);
-    p.group_m = p.tiles_m < 4 ? p.tiles_m : 4;
-    ka = make_args(a, p);
+    set_tiles(p, pr.M, ns, pr.nproj);
+    p.splits = 1;
+    p.kb_per_split = ka.kblocks;
+    fill(p);
   }
+  if (p.splits > 1 && (!workspace || (int64_t)p.tiles_m * p.tiles_n > kMaxSplitTiles ||
+                       gemm_workspace_bytes(p) >= (1ull << 31)))
+    return hipErrorInvalidValue;
   switch (p.cfg) {
     case kV3M128N256: return launch_v3_t<128, 256, 1, 4, 2, 2>(ka, stream);
     case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3>(ka, stream);
     case kV3M128N128S3: return launch_v3_t<128, 128, 1, 4, 3, 2>(ka, stream);
     case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2>(ka, stream);
-    case kDmaM128N128: return launch_dma_t<128, 128, 1, 4, 3, 1>(ka, stream);
+    case kV3M256N256: return launch_v3_t<256, 256, 2, 4, 2, 1>(ka, stream);
+    case kDmaM128N128: return launch_dma_t<128, 128, 1, 4, 3>(ka, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -330,7 +330,7 @@ hipError_t launch_t(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t str
   return hipGetLastError();
 }
 
-GemvKernelArgs make_args(const GemvProblem& pr, const GemvPlan& p, void* workspace) {
+GemvKernelArgs make_args(const LinearProblem& pr, const GemvPlan& p, void* workspace) {
   GemvKernelArgs ka;
   ka.x = pr.x;
   ka.ldx = pr.ldx;
@@ -415,7 +415,7 @@ size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj) 
   return (size_t)p.splits * (size_t)M * (size_t)np * sizeof(float);
 }
 
-hipError_t launch_gemv(const GemvProblem& pr, const GemvPlan& p, void* workspace,
+hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspace,
                        hipStream_t stream) {
   if (pr.nproj < 1 || pr.nproj > kMaxProj) return hipErrorInvalidValue;
   const GemvKernelArgs ka = make_args(pr, p, workspace);

@@ -12,23 +12,10 @@ namespace rf {
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
-// Arguments of one W8A16 linear call, already validated.
-struct LinearArgs {
-  const _Float16* x;
-  int64_t ldx;
-  const uint8_t* w;      // TILE16X64 packed
-  const _Float16* scale; // [N]
-  const _Float16* bias;  // [N] or nullptr
-  _Float16* y;
-  int64_t ldy;
-  int M, N, K;
-  int kblocks;  // Kp / 64
-  int nstrips;  // Np / 16
-};
-
-// One projection of a GEMV launch (weights, per-channel scale, optional bias,
-// output) and a launch of up to RF_W8A16_MAX_PROJ projections sharing x.
-struct GemvProjection {
+// One projection of a launch (weights, per-channel scale, optional bias,
+// output) and a launch of up to RF_W8A16_MAX_PROJ projections sharing x,
+// already validated.
+struct Projection {
   const uint8_t* w;      // TILE16X64 packed
   const _Float16* scale; // [N]
   const _Float16* bias;  // [N] or nullptr
@@ -37,12 +24,12 @@ struct GemvProjection {
   int N;
 };
 
-struct GemvProblem {
+struct LinearProblem {
   const _Float16* x;
   int64_t ldx;
   int M, K;
   int nproj;
-  GemvProjection proj[RF_W8A16_MAX_PROJ];
+  Projection proj[RF_W8A16_MAX_PROJ];
 };
 
 // Decode GEMV / skinny-GEMM launch plan (M <= 64).
@@ -59,8 +46,10 @@ struct GemvPlan {
 struct GemmPlan {
   int cfg;       // tile configuration id (w8a16_gemm.hip)
   int bm, bn;    // workgroup tile
-  int tiles_m, tiles_n;
+  int tiles_m, tiles_n;  // tiles_n summed over the launch's projections
   int group_m;   // output-tile rows per scheduling group
+  int splits;    // K splits across workgroups (1 = no workspace use)
+  int kb_per_split;
 };
 
 struct DeviceInfo {
@@ -72,13 +61,16 @@ struct DeviceInfo {
 int device_info(DeviceInfo* out);
 
 GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev);
-GemmPlan plan_gemm(int M, int N, int K, const DeviceInfo& dev);
+GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev);
+// Workspace bytes past the RF_W8A16_WS_COUNTER_BYTES counter region.
 size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj);
+size_t gemm_workspace_bytes(const GemmPlan& p);
 
 // Launchers: return hipSuccess or the launch error.
-hipError_t launch_gemv(const GemvProblem& pr, const GemvPlan& p, void* workspace,
+hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspace,
                        hipStream_t stream);
-hipError_t launch_gemm(const LinearArgs& a, const GemmPlan& p, hipStream_t stream);
+hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& p, void* workspace,
+                       hipStream_t stream);
 hipError_t launch_pack(const int8_t* q, int64_t N, int64_t K, int64_t ldq,
                        uint8_t* dst, hipStream_t stream);
 

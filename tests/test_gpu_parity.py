@@ -281,13 +281,21 @@ def test_gemv_every_planner_rule(m, n, k):
     assert (y1.view(np.uint16) == y2.view(np.uint16)).all()
 
 
-# One shape per rule of the GEMM planner (w8a16_gemm.hip plan_gemm).
+# One shape per rule of the GEMM planner (w8a16_gemm.hip plan_gemm), with a
+# 256-CU MI355X: tiles = ceil(M/BM) * ceil(N/BN); a K split when tiles are
+# fewer than CUs x workgroups/CU and K has >= 2 x 16 blocks of 64.
 GEMM_POLICY = [
     (100, 520, 1032),    # M < 128: 64x256 tiles
     (1024, 8200, 264),   # M >= 1024, N >= 8192: 128x256 tiles, 2 workgroups/CU
     (1100, 1000, 520),   # M >= 1024, N < 8192: 128x128 tiles, 3 workgroups/CU
+    (1024, 16384, 128),  # M >= 1024, 256x256 tiles fill whole rounds (4 x 64 = 256)
+    (1025, 65300, 72),   # the same rule on ragged M, N, K (5 x 256 = 1280 tiles)
     (200, 16400, 136),   # 128 <= M < 1024, N >= 16384: 128x256 tiles
     (300, 384, 1024),    # 128 <= M < 1024, N < 16384: 128x128 tiles, 3 stages
+    (300, 384, 4096),    # 9 tiles, 64 K blocks: 4-way K split of 16 blocks
+    (200, 1000, 2056),   # 16 tiles, 33 K blocks: 2-way split, K tail in split 1
+    (100, 520, 4096),    # M < 128: 6 tiles, 4-way K split
+    (1024, 2048, 8192),  # M >= 1024: 128 tiles of 128x128, 6-way K split
 ]
 
 
@@ -297,7 +305,33 @@ def test_gemm_every_planner_rule(m, n, k):
     x, q, s, b = make_case(m, n, k, seed=18, bias=True)
     assert rf.select_kernel(m, n, k) == rf.KERNEL_GEMM
     rows = None if m <= 300 else np.random.default_rng(m).choice(m, 128, replace=False)
-    assert_parity(run_gpu(x, q, s, b), x, q, s, b, rows=rows, label=f"gemm policy {m}x{n}x{k}")
+    packed = rf.pack_weight(_to_dev(q))
+    y1 = run_gpu(x, q, s, b, packed=packed)
+    assert_parity(y1, x, q, s, b, rows=rows, label=f"gemm policy {m}x{n}x{k}")
+    y2 = run_gpu(x, q, s, b, packed=packed)  # split-K: counters left zeroed, same sum order
+    assert (y1.view(np.uint16) == y2.view(np.uint16)).all()
+
+
+def test_gemm_split_k_matches_unsplit_order_free():
+    """The K-split GEMM sums its fp32 partials in split order: bit-identical over
+    repeated calls and interleaved with other shapes, and within tolerance of the
+    GEMV on the same inputs (M=64 forced to the GEMM: 4 tiles of 64x256, 8-way split)."""
+    m, n, k = 64, 1024, 8192
+    _say(f"gemm split-K vs gemv M={m} N={n} K={k}")
+    x, q, s, b = make_case(m, n, k, seed=31, bias=True)
+    packed = rf.pack_weight(_to_dev(q))
+    xd, sd, bd = _to_dev(x), _to_dev(s), _to_dev(b)
+    first = rf.linear(xd, packed, sd, bd, kernel=rf.KERNEL_GEMM)
+    for i in range(3):
+        other = make_case(150, 300, 2048, seed=32 + i)
+        run_gpu(*other)  # another split shape on the same workspace in between
+        again = rf.linear(xd, packed, sd, bd, kernel=rf.KERNEL_GEMM)
+        assert torch.equal(first, again)
+    y = first.cpu().numpy()
+    assert_parity(y, x, q, s, b, label="gemm split-K")
+    g = rf.linear(xd, packed, sd, bd, kernel=rf.KERNEL_GEMV).cpu().numpy()
+    rep = o.check_tolerance(y, g, o.oracle_fp64(x, q, s, b))
+    assert rep.ok, f"gemm split-K vs gemv: {rep}"
 
 
 def test_gemm_fallback_when_row_stride_overflows_32bit_offsets():
@@ -450,6 +484,35 @@ def test_linear_multi_qkv_and_gate_up(m):
             single = rf.linear(xd, packed, _to_dev(s), None if b is None else _to_dev(b)).cpu().numpy()
             rep = o.check_tolerance(y, single, o.oracle_fp64(x, q, s, b))
             assert rep.ok, f"multi vs single: {rep}"
+
+
+def test_linear_multi_gemm_one_launch_ragged_split():
+    """M=1030 (GEMM), three projections of ragged widths sharing K=4104 (K tail)
+    in one launch: 117 tiles of 128x128 take a 4-way K split; one projection
+    has a bias.  Each output against the oracle and against a single call."""
+    m, k = 1030, 4104
+    ns = [(1000, False), (264, True), (136, False)]
+    x = o.make_activation(o.derive_seed(24, "x", m, k), m, k)
+    rows = np.random.default_rng(24).choice(m, 96, replace=False)
+    cases = []
+    for pi, (n, has_bias) in enumerate(ns):
+        q, s = make_weights(n, k, seed=240 + pi)
+        b = (o.normal(o.derive_seed(25, "b", n, pi), (n,)) * 0.1).astype(np.float16) if has_bias else None
+        cases.append((q, s, b, rf.pack_weight(_to_dev(q))))
+    xd = _to_dev(x)
+    _say(f"linear_multi gemm M={m} K={k} Ns={[n for n, _ in ns]}")
+    ys = rf.linear_multi(xd, [c[3] for c in cases], [_to_dev(c[1]) for c in cases],
+                         [None if c[2] is None else _to_dev(c[2]) for c in cases])
+    again = rf.linear_multi(xd, [c[3] for c in cases], [_to_dev(c[1]) for c in cases],
+                            [None if c[2] is None else _to_dev(c[2]) for c in cases])
+    torch.cuda.synchronize()
+    for pi, (q, s, b, packed) in enumerate(cases):
+        assert torch.equal(ys[pi], again[pi])
+        y = ys[pi].cpu().numpy()
+        assert_parity(y, x, q, s, b, rows=rows, label=f"multi gemm p{pi}")
+        single = rf.linear(xd, packed, _to_dev(s), None if b is None else _to_dev(b)).cpu().numpy()
+        rep = o.check_tolerance(y[rows], single[rows], o.oracle_fp64(x[rows], q, s, b))
+        assert rep.ok, f"multi gemm vs single: {rep}"
 
 
 def test_linear_multi_split_k_and_capi():
