@@ -67,6 +67,33 @@ __device__ __forceinline__ uint4 load_u4_stream(const void* p) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// One global_load_lds_dwordx4: every lane reads 16 bytes at `g`, the
+// wavefront's 64 x 16 bytes land lane-contiguously at LDS byte address
+// `lds` (wave-uniform, passed in M0).  Written as inline asm so the
+// compiler does not serialise every later LDS read behind it (it cannot
+// tell which LDS bytes a DMA writes); the kernels order the LDS traffic
+// themselves with explicit s_waitcnt vmcnt + s_barrier.  Nothing else in
+// these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Workgroup barrier without the memory fences __syncthreads() implies (a
+// release fence would wait for every DMA in flight).  The caller has
+// already waited for the loads whose data the other wavefronts read.
+__device__ __forceinline__ void barrier_lds() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+
 __device__ __forceinline__ half8 as_half8(uint4 v) {
   return __builtin_bit_cast(half8, v);
 }

@@ -111,24 +111,10 @@ __device__ __forceinline__ void tile_of(int bid, const GemmKernelArgs& a, int& t
   tn = r / gm;
 }
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-
-// One global_load_lds_dwordx4: every lane reads 16 bytes at `g`, the
-// wavefront's 64 x 16 bytes land lane-contiguously at LDS byte address
-// `lds` (wave-uniform, passed in M0).  Written as inline asm so the
-// compiler does not serialise every later LDS read behind it (it cannot
-// tell which LDS bytes a DMA writes); the kernels order the LDS traffic
-// themselves with explicit s_waitcnt vmcnt + s_barrier.  Nothing else in
-// these kernels uses M0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
-               : "memory", "m0");
-}
-
-// The same with a wave-uniform SGPR base and a per-lane 32-bit byte offset
-// (global_load_lds_dwordx4 voff, s[base]).
+// dma16 (w8a16_common.h) with a wave-uniform SGPR base and a per-lane
+// 32-bit byte offset (global_load_lds_dwordx4 voff, s[base]).
 __device__ __forceinline__ void dma16s(uint32_t voff, const void* sbase, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
@@ -141,15 +127,6 @@ __device__ __forceinline__ void dma16s(uint32_t voff, const void* sbase, uint32_
 // rows at chunk ^ 2; with this swizzle the accesses of every 8-, 16- and
 // 32-lane group cover distinct LDS banks (64 or 128 banks of 4 bytes).
 __device__ __forceinline__ int a_swizzle(int r) { return (r & 7) ^ (((r >> 3) & 1) * 5); }
-
-// Workgroup barrier without the memory fences __syncthreads() implies (a
-// release fence would wait for every DMA in flight).  The caller has
-// already waited for the loads whose data the other wavefronts read.
-__device__ __forceinline__ void barrier_lds() {
-  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  __asm__ volatile("" ::: "memory");
-}
 
 // Buffer resource over the split-K partials; accesses use sc1 (device-scope
 // coherent: written through / re-fetched past the issuing XCD's L2, the

@@ -78,62 +78,76 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Activation fragment of one tile for m-tile `mt` read from global memory:
-// x[m][k .. k+15] with m = 16*mt + lane%16, k = 64*kb + 16*(lane/16); rows
-// m >= M are zero.  K % 8 == 0, so a chunk that starts below K ends below K.
-template <int MT>
-__device__ __forceinline__ void load_x_global(const GemvKernelArgs& a, int kb, int lane,
-                                              half8 (&xa)[MT][2]) {
-  const int k = kb * kTileK + 16 * (lane >> 4);
+// Activation fragment of one tile for every m-tile read from global memory:
+// x[m][k .. k+15] with m = 16*mt + lane%16, k = 64*kb + 16*(lane/16).
+// Addresses are a wave-uniform base (x + 64*kb, scalar) plus a per-lane
+// 32-bit offset fixed for the whole call (xoff[mt]: row m, lane group), so a
+// load costs no vector address math.  Rows m >= M read row M-1 instead (their
+// MFMA output rows are never stored).  KT (K % 64 != 0, a launch-time
+// choice) clamps every chunk into the row and zeroes the chunks past K with
+// selects; without it the load path has no branch or select at all, which
+// keeps the compiler's load-wait bookkeeping exact (a branch around a load
+// makes it fall back to waiting for every load in flight).
+// K % 8 == 0, so a chunk that starts below K ends below K.
+template <int MT, bool KT>
+__device__ __forceinline__ void load_x_global(const GemvKernelArgs& a, int kb, const uint32_t (&xoff)[MT],
+                                              int lane, half8 (&xa)[MT][2]) {
+  const uint8_t* xb = reinterpret_cast<const uint8_t*>(a.x) + (int64_t)kb * (kTileK * 2);
+  if (!KT) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + (lane & 15);
-    uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-    if (m < a.M) {
-      const _Float16* p = a.x + (int64_t)m * a.ldx + k;
-      if (k < a.K) v0 = load_u4(p);
-      if (k + 8 < a.K) v1 = load_u4(p + 8);
+    for (int mt = 0; mt < MT; ++mt) {
+      xa[mt][0] = as_half8(load_u4(xb + xoff[mt]));
+      xa[mt][1] = as_half8(load_u4(xb + xoff[mt] + 16));
     }
-    xa[mt][0] = as_half8(v0);
-    xa[mt][1] = as_half8(v1);
+  } else {
+    const int k = kb * kTileK + 16 * (lane >> 4);
+    // byte offsets (<= 0) that pull each chunk back inside the row
+    const int d0 = (min(k, a.K - 8) - k) * 2, d1 = (min(k + 8, a.K - 8) - (k + 8)) * 2;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const half8 v0 = as_half8(load_u4(xb + xoff[mt] + d0));
+      const half8 v1 = as_half8(load_u4(xb + xoff[mt] + 16 + d1));
+      xa[mt][0] = k < a.K ? v0 : half8{};
+      xa[mt][1] = k + 8 < a.K ? v1 : half8{};
+    }
   }
 }
 
 // The same fragment read from the LDS copy of x (row pitch `pitch` bytes,
-// column 0 = first K position of the split; rows >= M are never read).
+// column 0 = first K position of the split; the copy is zero past K).  Rows
+// m >= M read row M-1; tiles past the split read tile kl_max and are zeroed.
 template <int MT>
-__device__ __forceinline__ void load_x_lds(const uint8_t* xs, int pitch, int M, int kl, int lane,
-                                           half8 (&xa)[MT][2]) {
-  const int k = kl * kTileK + 16 * (lane >> 4);
+__device__ __forceinline__ void load_x_lds(const uint8_t* xs, int pitch, int M, int kl, int kl_max,
+                                           int lane, half8 (&xa)[MT][2]) {
+  const bool valid = kl <= kl_max;
+  const int k = min(kl, kl_max) * kTileK + 16 * (lane >> 4);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + (lane & 15);
-    uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-    if (m < M) {
-      const uint8_t* p = xs + m * pitch + k * 2;
-      v0 = *reinterpret_cast<const uint4*>(p);
-      v1 = *reinterpret_cast<const uint4*>(p + 16);
-    }
-    xa[mt][0] = as_half8(v0);
-    xa[mt][1] = as_half8(v1);
+    const int m = min(mt * 16 + (lane & 15), M - 1);
+    const uint8_t* p = xs + m * pitch + k * 2;
+    const half8 v0 = as_half8(*reinterpret_cast<const uint4*>(p));
+    const half8 v1 = as_half8(*reinterpret_cast<const uint4*>(p + 16));
+    xa[mt][0] = valid ? v0 : half8{};
+    xa[mt][1] = valid ? v1 : half8{};
   }
 }
 
 // Dynamic LDS bytes the kernel needs: max(x copy, cross-wave reduction).
 inline size_t gemv_lds_bytes(int MT, int NS, int W, bool XL, int M, int kb_per_split) {
   const size_t red = (size_t)W * MT * NS * kWave * sizeof(floatx4);
-  const size_t xb = XL ? (size_t)M * (size_t)(kb_per_split * kTileK * 2 + 16) : 0;
+  // x copy, rounded up to whole 1 KB DMA chunks
+  const size_t xb = XL ? ((size_t)M * (size_t)(kb_per_split * kTileK * 2 + 16) + 1023) / 1024 * 1024 : 0;
   return red > xb ? red : xb;
 }
 
-template <int MT, int NS, int W, int U, bool XL, bool NT>
+template <int MT, int NS, int W, int U, bool XL, bool NT, bool KT>
 __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int kThreads = W * kWave;
   constexpr int T = MT * NS;  // 16x16 output tiles per workgroup
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int group = blockIdx.x;
   const int split = blockIdx.y;
   // Projection of this workgroup (uniform across it).
@@ -154,37 +168,44 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   const int kb1 = min(kb0 + a.kb_per_split, a.kblocks);
   const int ntiles = kb1 - kb0;
 
-  // ---- stage x[0:M, split's K range] in LDS -----------------------------
-  int pitch = 0;
-  if (XL) {
-    pitch = ntiles * kTileK * 2 + 16;  // +16 B: rows start on different banks
-    const int row_chunks = ntiles * (kTileK / 8);
-    const int total = a.M * row_chunks;
-    for (int c = tid; c < total; c += kThreads) {
-      const int m = c / row_chunks, cc = c - m * row_chunks;
-      const int k = kb0 * kTileK + cc * 8;
-      const uint4 v = k < a.K ? load_u4(a.x + (int64_t)m * a.ldx + k) : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(smem + m * pitch + cc * 16) = v;
-    }
-    __syncthreads();
-  }
+  // LDS row pitch of the x copy: 128 B per tile (+16 B in the register-
+  // staged K-tail path, so rows start on different banks).
+  const int pitch = XL ? ntiles * kTileK * 2 + (KT ? 16 : 0) : 0;
 
-  floatx4 acc[MT][NS];
+  // CH independent accumulator chains (the two K halves of a tile, and
+  // alternate tiles when registers allow): a single chain would make every
+  // MFMA wait for the previous one, and the wavefront could not issue its
+  // next loads meanwhile.  The chains are summed in a fixed order at the end.
+  constexpr int CH = (MT * NS <= 2) ? 4 : 2;
+  floatx4 accs[CH][MT][NS];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int s = 0; s < NS; ++s) acc[mt][s] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s = 0; s < NS; ++s) accs[c][mt][s] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Strip s of this group exists iff strip0 + s < nstrips (uniform per WG).
-  bool strip_ok[NS];
-  const uint8_t* wbase[NS];
+  // Strip s of this group exists iff strip0 + s < nstrips (uniform per WG);
+  // a missing strip loads the projection's last strip instead and its
+  // outputs are never stored.  Tile bases are wave-uniform (scalar); lane l
+  // reads bytes [16*l, 16*l + 16) of a tile.
+  const uint8_t* wstrip[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    strip_ok[s] = (strip0 + s) < P_nstrips;
-    wbase[s] = P_w + ((int64_t)(strip0 + s) * a.kblocks + kb0) * kTileBytes + lane * 16;
+    const int strip = min(strip0 + s, P_nstrips - 1);
+    wstrip[s] = P_w + ((int64_t)strip * a.kblocks + kb0) * kTileBytes;
   }
+  const uint32_t woff = lane * 16;
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xoff[mt] = (uint32_t)(min(mt * 16 + (lane & 15), a.M - 1) * a.ldx * 2) + 32 * (lane >> 4);
 
   // Tiles of this wavefront: local index kl = wave + W*i, i in [0, my).
+  // Every load below is unconditional: a tile past the split (the last
+  // stage may be partial) loads tile ntiles-1 and is skipped in compute (a
+  // wave-uniform branch with no loads in it, so in-flight loads are not
+  // waited for; overwriting their registers would be).
   const int my = ntiles > wave ? (ntiles - wave + W - 1) / W : 0;
   const int stages = (my + U - 1) / U;
 
@@ -195,24 +216,13 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kl = wave + W * (st * U + u);
-      const bool ok = kl < ntiles;
+      const int klc = min(kl, ntiles - 1);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        if (ok && strip_ok[s]) {
-          const uint8_t* p = wbase[s] + (int64_t)kl * kTileBytes;
-          wv[u][s] = NT ? load_u4_stream(p) : load_u4(p);
-        } else {
-          wv[u][s] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-        }
+        const uint8_t* p = wstrip[s] + (int64_t)klc * kTileBytes + woff;
+        wv[u][s] = NT ? load_u4_stream(p) : load_u4(p);
       }
-      if (!XL) {
-        if (ok) {
-          load_x_global<MT>(a, kb0 + kl, lane, xv[XL ? 0 : u]);
-        } else {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) xv[XL ? 0 : u][mt][0] = xv[XL ? 0 : u][mt][1] = half8{};
-        }
-      }
+      if (!XL) load_x_global<MT, KT>(a, kb0 + klc, xoff, lane, xv[XL ? 0 : u]);
     }
   };
 
@@ -220,9 +230,9 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kl = wave + W * (st * U + u);
-      if (kl >= ntiles) break;  // uniform across the wavefront
+      if (kl >= ntiles) break;  // wave-uniform
       half8 xl[MT][2];
-      if (XL) load_x_lds<MT>(smem, pitch, a.M, kl, lane, xl);
+      if (XL) load_x_lds<MT>(smem, pitch, a.M, kl, ntiles - 1, lane, xl);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const half8 b0 = dequant8(wv[u][s].x, wv[u][s].y);
@@ -231,22 +241,75 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
         for (int mt = 0; mt < MT; ++mt) {
           const half8 x0 = XL ? xl[mt][0] : xv[XL ? 0 : u][mt][0];
           const half8 x1 = XL ? xl[mt][1] : xv[XL ? 0 : u][mt][1];
-          acc[mt][s] = mfma16x16x32(x0, b0, acc[mt][s]);
-          acc[mt][s] = mfma16x16x32(x1, b1, acc[mt][s]);
+          const int c = (2 * u) % CH;  // chains c (first K half), c+1 (second)
+          accs[c][mt][s] = mfma16x16x32(x0, b0, accs[c][mt][s]);
+          accs[c + 1][mt][s] = mfma16x16x32(x1, b1, accs[c + 1][mt][s]);
         }
       }
     }
   };
 
-  // Two-stage pipeline, unrolled by two so the buffers never move.
-  if (stages > 0) load_stage(0, wA, xA);
-  for (int st = 0; st < stages; st += 2) {
-    if (st + 1 < stages) load_stage(st + 1, wB, xB);
-    compute_stage(st, wA, xA);
-    if (st + 1 >= stages) break;
-    if (st + 2 < stages) load_stage(st + 2, wA, xA);
-    compute_stage(st + 1, wB, xB);
+  // x[0:M, split's K range] -> LDS by DMA (K % 64 == 0: no zero fill):
+  // 1 KB chunk j of the row-major copy (pitch = 128 B per tile) is written by
+  // wavefront j % W; lanes past the end read the last chunk again and land
+  // in the rounded-up tail of the allocation.  Issued first: the weight
+  // loads below may then stay in flight while it is waited for.
+  if (XL && !KT) {
+    const int total = a.M * pitch;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)smem;
+    for (int j = wave; j * 1024 < total; j += W) {
+      const int pb = min(j * 1024 + lane * 16, total - 16);
+      const int m = pb / pitch, c = pb - m * pitch;
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(a.x + (int64_t)m * a.ldx + kb0 * kTileK) + c;
+      dma16(src, lds0 + j * 1024);
+    }
   }
+  // The first two stages of weight tiles go out before anything waits.
+  if (stages > 0) load_stage(0, wA, xA);
+  if (stages > 1) load_stage(1, wB, xB);
+
+  // ---- stage x[0:M, split's K range] in LDS (zero past K) ----------------
+  if (XL && KT) {
+    // Columns past K need zeros: staged through registers (after the first
+    // weight tiles went out, so the two round trips overlap).
+    const int row_chunks = ntiles * (kTileK / 8);
+    const int total = a.M * row_chunks;
+    for (int c = tid; c < total; c += kThreads) {
+      const int m = c / row_chunks, cc = c - m * row_chunks;
+      const int k = kb0 * kTileK + cc * 8;
+      const uint4 v = load_u4(a.x + (int64_t)m * a.ldx + min(k, a.K - 8));
+      *reinterpret_cast<uint4*>(smem + m * pitch + cc * 16) = k < a.K ? v : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+  } else if (XL) {
+    // The DMAs were issued before the weight loads (xdma above): wait for
+    // this wave's share (every load issued after them may stay in flight),
+    // then for everyone's.
+    if (stages > 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * U * NS) : "memory");
+    else if (stages > 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(U * NS) : "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    barrier_lds();
+  }
+
+  // Two-stage pipeline, unrolled by two so the buffers never move: a
+  // stage's buffer is refilled (two stages ahead) as soon as it is consumed.
+  for (int st = 0; st < stages; st += 2) {
+    compute_stage(st, wA, xA);
+    if (st + 2 < stages) load_stage(st + 2, wA, xA);
+    if (st + 1 >= stages) break;
+    compute_stage(st + 1, wB, xB);
+    if (st + 3 < stages) load_stage(st + 3, wB, xB);
+  }
+
+  floatx4 acc[MT][NS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      acc[mt][s] = accs[0][mt][s] + accs[1][mt][s];
+#pragma unroll
+      for (int c = 2; c < CH; c += 2) acc[mt][s] += accs[c][mt][s] + accs[c + 1][mt][s];
+    }
 
   // ---- cross-wavefront reduction through LDS (fixed order) --------------
   if (XL) __syncthreads();  // everyone is done with the x copy
@@ -325,8 +388,12 @@ hipError_t launch_t(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t str
   const size_t lds = gemv_lds_bytes(MT, NS, W, XL, ka.M, ka.kb_per_split);
   if (lds > 65536) return hipErrorInvalidValue;
   dim3 grid(p.groups, p.splits, 1);
-  hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, W, U, XL, NT>), grid, dim3(W * kWave), lds, stream,
-                     ka);
+  if ((ka.K % kTileK) != 0)  // K-tail variant: chunks past K are zeroed
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, W, U, XL, NT, true>), grid, dim3(W * kWave), lds,
+                       stream, ka);
+  else
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, W, U, XL, NT, false>), grid, dim3(W * kWave), lds,
+                       stream, ka);
   return hipGetLastError();
 }
 
@@ -372,20 +439,20 @@ GemvKernelArgs make_args(const LinearProblem& pr, const GemvPlan& p, void* works
 // Kernel configurations the planner chooses from (all stream weights with
 // non-temporal loads).  Measured on MI355X over the BASELINE decode shapes.
 enum GemvCfgId {
-  kG1x1W16U4,   // MT=1 NS=1 W=16 U=4
-  kG1x1W16U2,   // MT=1 NS=1 W=16 U=2   (long K)
-  kG1x1W8U4XL,  // MT=1 NS=1 W=8  U=4, x staged in LDS (many strips)
-  kG1x1W4U4,    // MT=1 NS=1 W=4  U=4
-  kG1x2W16U2,   // MT=1 NS=2 W=16 U=2
-  kG1x4W8U2,    // MT=1 NS=4 W=8  U=2   (M 5..16: x fragment reused 4x)
-  kG1x4W4U2,    // MT=1 NS=4 W=4  U=2
-  kG1x2W8U2,    // MT=1 NS=2 W=8  U=2
-  kG1x2W4U4,    // MT=1 NS=2 W=4  U=4
-  kG2x4W4U2,    // MT=2 NS=4 W=4  U=2
-  kG2x2W8U1,    // MT=2 NS=2 W=8  U=1
-  kG2x1W8U4,    // MT=2 NS=1 W=8  U=4
-  kG4x2W8U1,    // MT=4 NS=2 W=8  U=1
-  kG4x2W4U1,    // MT=4 NS=2 W=4  U=1
+  kG1x1W16U4,    // MT=1 NS=1 W=16 U=4
+  kG1x1W16U4XL,  // MT=1 NS=1 W=16 U=4, x staged in LDS (M = 1, short K)
+  kG1x1W8U4,     // MT=1 NS=1 W=8  U=4   (long K)
+  kG1x1W8U4XL,   // MT=1 NS=1 W=8  U=4, x staged in LDS (many strips / long K)
+  kG1x1W4U4,     // MT=1 NS=1 W=4  U=4
+  kG1x2W16U2,    // MT=1 NS=2 W=16 U=2
+  kG1x4W8U2,     // MT=1 NS=4 W=8  U=2   (M 5..16: x fragment reused 4x)
+  kG1x4W4U2,     // MT=1 NS=4 W=4  U=2
+  kG1x2W8U2,     // MT=1 NS=2 W=8  U=2
+  kG2x4W4U2,     // MT=2 NS=4 W=4  U=2
+  kG2x2W8U1,     // MT=2 NS=2 W=8  U=1
+  kG2x1W8U4,     // MT=2 NS=1 W=8  U=4
+  kG4x2W8U1,     // MT=4 NS=2 W=8  U=1
+  kG4x2W4U1,     // MT=4 NS=2 W=4  U=1
   kGemvCfgCount
 };
 
@@ -395,10 +462,9 @@ struct GemvCfgDesc {
 };
 
 constexpr GemvCfgDesc kGemvCfgs[kGemvCfgCount] = {
-    {1, 1, 16, false}, {1, 1, 16, false}, {1, 1, 8, true}, {1, 1, 4, false},
-    {1, 2, 16, false}, {1, 4, 8, false},  {1, 4, 4, false}, {1, 2, 8, false},
-    {1, 2, 4, false},  {2, 4, 4, false},
-    {2, 2, 8, false},  {2, 1, 8, false},  {4, 2, 8, false}, {4, 2, 4, false},
+    {1, 1, 16, false}, {1, 1, 16, true}, {1, 1, 8, false}, {1, 1, 8, true}, {1, 1, 4, false},
+    {1, 2, 16, false}, {1, 4, 8, false}, {1, 4, 4, false}, {1, 2, 8, false},
+    {2, 4, 4, false},  {2, 2, 8, false}, {2, 1, 8, false}, {4, 2, 8, false}, {4, 2, 4, false},
 };
 
 bool lds_fits(int cfg, int M, int kb_per_split) {
@@ -421,14 +487,14 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
   const GemvKernelArgs ka = make_args(pr, p, workspace);
   switch (p.cfg) {
     case kG1x1W16U4: return launch_t<1, 1, 16, 4, false, true>(ka, p, stream);
-    case kG1x1W16U2: return launch_t<1, 1, 16, 2, false, true>(ka, p, stream);
+    case kG1x1W16U4XL: return launch_t<1, 1, 16, 4, true, true>(ka, p, stream);
+    case kG1x1W8U4: return launch_t<1, 1, 8, 4, false, true>(ka, p, stream);
     case kG1x1W8U4XL: return launch_t<1, 1, 8, 4, true, true>(ka, p, stream);
     case kG1x1W4U4: return launch_t<1, 1, 4, 4, false, true>(ka, p, stream);
     case kG1x2W16U2: return launch_t<1, 2, 16, 2, false, true>(ka, p, stream);
     case kG1x4W8U2: return launch_t<1, 4, 8, 2, false, true>(ka, p, stream);
     case kG1x4W4U2: return launch_t<1, 4, 4, 2, false, true>(ka, p, stream);
     case kG1x2W8U2: return launch_t<1, 2, 8, 2, false, true>(ka, p, stream);
-    case kG1x2W4U4: return launch_t<1, 2, 4, 4, false, true>(ka, p, stream);
     case kG2x4W4U2: return launch_t<2, 4, 4, 2, false, true>(ka, p, stream);
     case kG2x2W8U1: return launch_t<2, 2, 8, 1, false, true>(ka, p, stream);
     case kG2x1W8U4: return launch_t<2, 1, 8, 4, false, true>(ka, p, stream);
@@ -457,17 +523,20 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   auto strips_ge = [&](int n256) { return (int64_t)nstrips * 256 >= (int64_t)n256 * cu; };
   int cfg, splits = 1;
   if (M <= 4) {
+    // x staged in LDS (one DMA copy per workgroup instead of every
+    // wavefront re-reading the same L2 lines) pays off at M <= 2.
     if (strips_ge(640)) {
-      // Many strips: x staged in LDS at M <= 2; two strips per workgroup
-      // sharing the fragment at M 3..4 once there are >= 1024 strips.
-      cfg = (M >= 3 && strips_ge(1024)) ? kG1x2W4U4 : kG1x1W8U4XL;
+      // Many strips: two strips per workgroup share the x fragment at M 3..4.
+      cfg = M >= 3 ? kG1x2W8U2 : kG1x1W8U4XL;
       if (!lds_fits(cfg, M, kblocks)) cfg = kG1x1W4U4;
     } else if (strips_ge(257)) {
       cfg = kG1x2W16U2;
     } else if (kblocks >= 128) {
-      cfg = kG1x1W16U2;
+      cfg = (M == 1 && lds_fits(kG1x1W8U4XL, M, kblocks)) ? kG1x1W8U4XL : kG1x1W8U4;
     } else {
-      cfg = kG1x1W16U4;
+      // (short K: one tile per wavefront does not amortize the staging wait)
+      cfg = (M == 1 && kblocks >= 48 && lds_fits(kG1x1W16U4XL, M, kblocks)) ? kG1x1W16U4XL
+                                                                             : kG1x1W16U4;
     }
   } else if (M <= 16) {
     if (strips_ge(2048)) {
@@ -477,7 +546,7 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     } else if (strips_ge(512)) {
       cfg = kG1x4W8U2;
     } else if (strips_ge(257)) {
-      cfg = kG1x2W8U2;
+      cfg = kG1x2W16U2;
     } else if (kblocks >= 128) {
       cfg = kG1x4W8U2;
       splits = 4;

@@ -247,16 +247,21 @@ def test_edge_shapes(m, n, k, bias):
 # One shape per rule of the GEMV planner (w8a16_gemv.hip plan_gemv), so every
 # kernel configuration it can pick runs at least once.
 GEMV_POLICY = [
-    (2, 10240, 512),   # M<=4, >=640 strips: x staged in LDS
-    (4, 10240, 8256),  # same rule, x does not fit in LDS: plain 4-wave config
-    (3, 16384, 512),   # M 3..4, >=1024 strips: two strips per 4-wave workgroup
+    (2, 10240, 512),   # M<=2, >=640 strips: x staged in LDS by DMA
+    (2, 10240, 16448), # same rule, x does not fit in LDS: plain 4-wave config
+    (3, 16384, 512),   # M 3..4, >=640 strips: two strips per 8-wave workgroup
+    (4, 10240, 8256),  # the same at long K
     (1, 5000, 320),    # M<=4, 257..639 strips: two strips per workgroup
-    (3, 512, 8192),    # M<=4, long K
-    (1, 512, 1024),    # M<=4, default
+    (1, 512, 8192),    # M=1, long K: x in LDS, 8 wavefronts
+    (3, 512, 8192),    # M<=4, long K: 8 wavefronts, x from global memory
+    (1, 512, 4096),    # M=1, default: x in LDS, 16 wavefronts
+    (1, 300, 3136),    # same, x copy ends mid-way through a 1 KB DMA chunk
+    (1, 520, 3080),    # same, K % 64 != 0: x staged through registers, zero past K
+    (1, 512, 1024),    # M<=4, default (short K, or M > 1)
     (8, 32768, 128),   # M 5..16, >=2048 strips
     (16, 16384, 256),  # M 5..16, >=1024 strips: two strips per 8-wave workgroup
     (12, 8192, 256),   # M 5..16, >=512 strips
-    (10, 5000, 512),   # M 5..16, 257..511 strips: two strips per 8-wave workgroup
+    (10, 5000, 512),   # M 5..16, 257..511 strips: two strips per 16-wave workgroup
     (16, 1024, 8192),  # M 5..16, long K: 4-way K split
     (9, 1000, 1024),   # M 5..16, <=64 strips: 4-way K split
     (16, 2048, 1024),  # M 5..16, default
