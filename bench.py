@@ -209,12 +209,18 @@ def bench_decode(torch, rf, steps, warmup):
     del layers
     torch.cuda.empty_cache()
     fused_launches = steps * len(DECODE_M) * 4
+    # Algorithmic bytes of the fused step: a shared input is read once per launch.
+    fused_bytes = 0
+    for m in DECODE_M:
+        for idxs in ((0, 1, 2), (3,), (4, 5), (6,)):
+            k = QWEN3_8B[idxs[0]][2]
+            fused_bytes += sum(nbytes(m, QWEN3_8B[i][1], k) - 2 * m * k for i in idxs) + 2 * m * k
     return {
-        "GBps": step_bytes * steps / (tf.ms * 1e-3) / 1e9,
+        "GBps": fused_bytes * steps / (tf.ms * 1e-3) / 1e9,
         "ms_per_step": tf.ms / steps,
         "launches": fused_launches,
         "avg_launch_us": tf.ms * 1e3 / fused_launches,
-        "avg_bytes_per_launch": step_bytes / (len(DECODE_M) * 4),
+        "avg_bytes_per_launch": fused_bytes / (len(DECODE_M) * 4),
         "per_op_GBps": step_bytes * steps / (t.ms * 1e-3) / 1e9,
         "per_op_ms_per_step": t.ms / steps,
         "per_op_avg_launch_us": t.ms * 1e3 / launches,
