@@ -313,8 +313,14 @@ def bench_other_configs(torch, rf):
         x = torch.randn(m, 5120, device="cuda").half()
         y = torch.empty(m, 151936, device="cuda", dtype=torch.float16)
         us = per_launch_us(torch, lambda c: rf.linear_into(x, c[3], c[4], None, y), [head], 10)
+        # greedy decode: the token ids, by the fused-argmax launch, and by the logits
+        # launch followed by torch.argmax
+        us_am = per_launch_us(torch, lambda c: rf.linear_argmax(x, c[3], c[4]), [head], 10)
+        us_two = per_launch_us(torch, lambda c: (rf.linear_into(x, c[3], c[4], None, y),
+                                                  y.argmax(-1)), [head], 10)
         rows.append({"M": m, "us": round(us, 1),
-                     "GBps": round(nbytes(m, 151936, 5120) / (us * 1e-6) / 1e9, 1)})
+                     "GBps": round(nbytes(m, 151936, 5120) / (us * 1e-6) / 1e9, 1),
+                     "argmax_fused_us": round(us_am, 1), "logits_then_argmax_us": round(us_two, 1)})
     out["cfg2_lm_head"] = rows
     del head
     torch.cuda.empty_cache()

@@ -117,7 +117,7 @@ typedef struct rf_w8a16_proj {
  * on the current device (fp32 split-K partials of the GEMV or the GEMM).
  * The first RF_W8A16_WS_COUNTER_BYTES bytes are split-K arrival counters:
  * they must be zero before the first call that uses the buffer, and every
- * successful call leaves them zero again. */
+ * successful call leaves them zero again.  The bytes after them are scratch. */
 size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 #define RF_W8A16_WS_COUNTER_BYTES 65536
 
@@ -155,6 +155,26 @@ int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed,
 int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w8a16_proj* projs,
                           int32_t count, int64_t M, int64_t K, int32_t kernel, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/* Greedy-decode lm_head: index[m] = argmax_n fp16(y[m][n]) of
+ * y = x . dequant(w)^T (+ bias), int32, the lowest n among equal maxima (NaN
+ * counts as the largest value, -0 equals +0), for 1 <= M <= 64 (the decode
+ * GEMV).  The per-row argmax is folded into the GEMV epilogue, so the
+ * logits need not be written or read again; `y` (fp16 [M, ldy], ldy >= N)
+ * may be NULL, otherwise the logits are stored as by rf_w8a16_linear.
+ *   workspace: >= rf_w8a16_workspace_bytes_argmax(M,N,K) bytes, counter
+ *              region zeroed as for rf_w8a16_linear.  Two launches: the GEMV
+ *              leaves each workgroup's best per-row key in the workspace, a
+ *              second kernel reduces them.
+ * Other arguments as rf_w8a16_linear.  Returns RF_W8A16_EKERNEL for M > 64.
+ * Replaces the decode lm_head GEMM + argmax pair (src/fused/rpu_qwen3_model.h:
+ * 3653-3690 writes the logits; src/ops/rpu_argmax.cpp:485-640 reduces them,
+ * int32 result, first index among ties). */
+int rf_w8a16_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int32_t layout,
+                           const void* scale, const void* bias, void* y, int64_t ldy,
+                           int32_t* index, int64_t M, int64_t N, int64_t K, void* workspace,
+                           size_t workspace_bytes, void* stream);
+size_t rf_w8a16_workspace_bytes_argmax(int64_t M, int64_t N, int64_t K);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -35,6 +35,7 @@ from .ops import (  # noqa: E402
     KERNEL_GEMM,
     KERNEL_GEMV,
     linear,
+    linear_argmax,
     linear_into,
     linear_multi,
     pack_weight,
@@ -54,6 +55,7 @@ __all__ = [
     "W8A16Linear",
     "dequantize_linear_per_channel",
     "linear",
+    "linear_argmax",
     "linear_into",
     "linear_multi",
     "pack_weight",

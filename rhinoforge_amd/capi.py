@@ -58,6 +58,11 @@ SIGNATURES = {
                                    _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64,
                                    _c.c_int64, _c.c_int64, _c.c_int64, _c.c_int32,
                                    _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "rf_w8a16_linear_argmax": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int32,
+                                          _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64,
+                                          _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
+                                          _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "rf_w8a16_workspace_bytes_argmax": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int64]),
 }
 
 _lib = None

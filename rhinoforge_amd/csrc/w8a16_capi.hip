@@ -7,6 +7,7 @@
 // Unlike the RPU the kernels accept every M, N >= 1 and K % 8 == 0: there is
 // no core partition to satisfy (runtime/weights.py:97-135), only the
 // 16-byte activation-row alignment of a 128-bit load.
+#include <limits.h>
 #include <string.h>
 
 #include <atomic>
@@ -290,6 +291,63 @@ int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed, int32_t la
   q.N = N;
   return rf_w8a16_linear_multi(x, ldx, layout, &q, 1, M, K, kernel, workspace, workspace_bytes,
                                stream);
+}
+
+size_t rf_w8a16_workspace_bytes_argmax(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > 64 || check_nk(N, K) != RF_W8A16_OK || N > INT32_MAX - 1) return 0;
+  rf::DeviceInfo dev;
+  if (rf::device_info(&dev) != RF_W8A16_OK) {
+    dev.cus = 256;
+    dev.gfx950 = false;
+  }
+  const int n32 = (int)N;
+  const rf::GemvPlan p = rf::plan_gemv((int)M, &n32, 1, (int)K, dev);
+  return RF_W8A16_WS_COUNTER_BYTES +
+         (size_t)rf::round_up((int64_t)rf::gemv_workspace_bytes(p, (int)M, &n32, 1), 256) +
+         rf::argmax_slot_bytes(p, (int)M);
+}
+
+int rf_w8a16_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int32_t layout,
+                           const void* scale, const void* bias, void* y, int64_t ldy,
+                           int32_t* index, int64_t M, int64_t N, int64_t K, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (!x || !w_packed || !scale || !index) return RF_W8A16_EINVAL;
+  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK || ldx < K) return RF_W8A16_EINVAL;
+  if (N > INT32_MAX - 1 || (y && ldy < N)) return RF_W8A16_EINVAL;
+  if (layout != RF_W8A16_LAYOUT_TILE16X64) return RF_W8A16_ELAYOUT;
+  if (K % 8 != 0 || ldx % 8 != 0 || !aligned(x, 16) || !aligned(w_packed, 16) ||
+      !aligned(scale, 2) || (bias && !aligned(bias, 2)) || (y && !aligned(y, 2)) ||
+      !aligned(index, 4))
+    return RF_W8A16_EALIGN;
+  if (M > 64) return RF_W8A16_EKERNEL;
+  rf::DeviceInfo dev;
+  int st = rf::device_info(&dev);
+  if (st != RF_W8A16_OK) return st;
+  if (!dev.gfx950) return RF_W8A16_EDEVICE;
+
+  rf::LinearProblem pr;
+  pr.x = static_cast<const _Float16*>(x);
+  pr.ldx = ldx;
+  pr.M = (int)M;
+  pr.K = (int)K;
+  pr.nproj = 1;
+  pr.proj[0].w = static_cast<const uint8_t*>(w_packed);
+  pr.proj[0].scale = static_cast<const _Float16*>(scale);
+  pr.proj[0].bias = static_cast<const _Float16*>(bias);
+  pr.proj[0].y = static_cast<_Float16*>(y);
+  pr.proj[0].ldy = y ? ldy : 0;
+  pr.proj[0].N = (int)N;
+  const int n32 = (int)N;
+  const rf::GemvPlan p = rf::plan_gemv(pr.M, &n32, 1, pr.K, dev);
+  const size_t slots_off = RF_W8A16_WS_COUNTER_BYTES +
+      (size_t)rf::round_up((int64_t)rf::gemv_workspace_bytes(p, pr.M, &n32, 1), 256);
+  const size_t need = slots_off + rf::argmax_slot_bytes(p, pr.M);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return RF_W8A16_EWORKSPACE;
+  rf::ArgmaxTarget am;  // per-workgroup keys in the scratch part of the workspace
+  am.slots = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(workspace) + slots_off);
+  am.index = index;
+  const hipError_t e = rf::launch_gemv(pr, p, workspace, static_cast<hipStream_t>(stream), &am);
+  return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
 }
 
 }  // extern "C"

@@ -553,7 +553,7 @@ namespace {
 
 constexpr int kMaxGemmSplits = 8;
 constexpr int kMinKbPerSplit = 16;  // 1024 input channels per split at least
-constexpr int kMaxSplitTiles = RF_W8A16_WS_COUNTER_BYTES / 4;
+constexpr int kMaxSplitTiles = kMaxSplitCounters;
 
 void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
   p.bm = kGemmTile[p.cfg][0];

@@ -39,7 +39,7 @@ namespace {
 
 constexpr int kMaxSplits = 16;
 constexpr int kMaxProj = RF_W8A16_MAX_PROJ;
-constexpr int kMaxGroupsSplit = RF_W8A16_WS_COUNTER_BYTES / 4;
+constexpr int kMaxGroupsSplit = kMaxSplitCounters;
 
 // One weight matrix of a launch.  Several projections that share the
 // activation x (q/k/v, or gate/up) run in one launch: workgroups are
@@ -68,7 +68,27 @@ struct GemvKernelArgs {
   int np;              // padded columns of all projections: row stride of partials
   float* partial;      // [splits][M][np]
   uint32_t* counters;  // [groups]
+  // Fused argmax (nullptr: none): every workgroup's best key per row,
+  // [M][gridDim.x], reduced by argmax_finish_kernel after this launch.
+  unsigned long long* amax_slots;
 };
+
+// Argmax key of output value v at column n: the fp16 value mapped to an
+// unsigned order (NaN above everything, -0 equal to +0, as torch.argmax
+// compares), +1 so that every key beats the reset value 0, in the high half;
+// ~n in the low half, so among equal values the lowest column wins.
+__device__ __forceinline__ unsigned long long argmax_key(_Float16 v, int n) {
+  uint32_t h = __builtin_bit_cast(uint16_t, v);
+  if (h == 0x8000u) h = 0;
+  uint32_t ord;
+  if ((h & 0x7fffu) > 0x7c00u) ord = 0xffffu;
+  else ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+  return ((unsigned long long)(ord + 1) << 32) | (uint32_t)(0xffffffffu - (uint32_t)n);
+}
+
+__device__ __forceinline__ int32_t argmax_index_of(unsigned long long key) {
+  return (int32_t)(0xffffffffu - (uint32_t)key);
+}
 
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -138,6 +158,70 @@ inline size_t gemv_lds_bytes(int MT, int NS, int W, bool XL, int M, int kb_per_s
   // x copy, rounded up to whole 1 KB DMA chunks
   const size_t xb = XL ? ((size_t)M * (size_t)(kb_per_split * kTileK * 2 + 16) + 1023) / 1024 * 1024 : 0;
   return red > xb ? red : xb;
+}
+
+// Split-K: each workgroup has stored its partials; the last one to arrive
+// at the group's counter sums every split in split order (deterministic),
+// applies scale and bias, stores fp16 (and feeds the fused argmax), and
+// re-zeroes the counter.  Returns whether this workgroup was the last.
+template <int NS>
+__device__ __forceinline__ bool split_k_reduce(const GemvKernelArgs& a, int group, int strip0,
+                                               int P_nstrips, int P_N, int P_col0,
+                                               const _Float16* P_scale, const _Float16* P_bias,
+                                               _Float16* P_y, int64_t P_ldy, bool amax,
+                                               unsigned long long* row_key, int tid, int nthreads) {
+  __shared__ uint32_t is_last;
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(&a.counters[group], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (prev == (uint32_t)(a.splits - 1)) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!is_last) return false;
+
+  const int nrows = min(NS, P_nstrips - strip0) * 16;
+  const int total = a.M * nrows;
+  for (int i = tid; i < total; i += nthreads) {
+    const int m = i / nrows;
+    const int n = strip0 * 16 + (i - m * nrows);
+    // Issue every split's load before summing (one memory round trip), then
+    // add in split order.
+    float part[kMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+      part[sp] = sp < a.splits
+                     ? load_coherent(&a.partial[((int64_t)sp * a.M + m) * a.np + P_col0 + n])
+                     : 0.f;
+    float sum = part[0];
+#pragma unroll
+    for (int sp = 1; sp < kMaxSplits; ++sp)
+      if (sp < a.splits) sum += part[sp];
+    if (n < P_N) {
+      const float sc = (float)P_scale[n];
+      const float bi = P_bias ? (float)P_bias[n] : 0.f;
+      const _Float16 v = (_Float16)__builtin_fmaf(sum, sc, bi);
+      if (P_y) P_y[(int64_t)m * P_ldy + n] = v;
+      if (amax)
+        __hip_atomic_fetch_max(&row_key[m], argmax_key(v, n), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+  if (tid == 0)
+    __hip_atomic_store(&a.counters[group], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+// Fused argmax: this workgroup's per-row best keys (row_key, LDS) go to its
+// own slots with plain stores -- no atomics on shared addresses, which with
+// thousands of workgroups on one row would serialise -- and the next launch
+// on the stream (argmax_finish_kernel) reduces the slots.
+__device__ __forceinline__ void argmax_store(const GemvKernelArgs& a, const unsigned long long* row_key,
+                                             int tid, int nthreads) {
+  __syncthreads();  // row_key complete
+  for (int m = tid; m < a.M; m += nthreads)
+    a.amax_slots[(int64_t)m * gridDim.x + blockIdx.x] = row_key[m];
 }
 
 template <int MT, int NS, int W, int U, bool XL, bool NT, bool KT>
@@ -312,6 +396,10 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
     }
 
   // ---- cross-wavefront reduction through LDS (fixed order) --------------
+  const bool amax = a.amax_slots != nullptr;  // fused argmax (M <= 64 rows)
+  __shared__ unsigned long long row_key[64];
+  if (amax)
+    for (int i = tid; i < 64; i += kThreads) row_key[i] = 0;
   if (XL) __syncthreads();  // everyone is done with the x copy
   float* red = reinterpret_cast<float*>(smem);  // [W][T][64 lanes][4]
 #pragma unroll
@@ -336,51 +424,63 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
       if (n < P_N) {
         const float sc = (float)P_scale[n];
         const float bi = P_bias ? (float)P_bias[n] : 0.f;
-        P_y[(int64_t)m * P_ldy + n] = (_Float16)__builtin_fmaf(sum, sc, bi);
+        const _Float16 v = (_Float16)__builtin_fmaf(sum, sc, bi);
+        if (P_y) P_y[(int64_t)m * P_ldy + n] = v;
+        if (amax)
+          __hip_atomic_fetch_max(&row_key[m], argmax_key(v, n), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
       }
     } else {
       store_coherent(&a.partial[((int64_t)split * a.M + m) * a.np + P_col0 + n], sum);
     }
   }
-  if (a.splits == 1) return;
+  if (a.splits > 1 && !split_k_reduce<NS>(a, group, strip0, P_nstrips, P_N, P_col0, P_scale,
+                                          P_bias, P_y, P_ldy, amax, row_key, tid, kThreads))
+    return;
+  if (amax) argmax_store(a, row_key, tid, kThreads);
+}
 
-  // ---- split-K: the last workgroup to arrive reduces in split order ------
-  __shared__ uint32_t is_last;
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(&a.counters[group], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == (uint32_t)(a.splits - 1)) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!is_last) return;
-
-  const int nrows = min(NS, P_nstrips - strip0) * 16;
-  const int total = a.M * nrows;
-  for (int i = tid; i < total; i += kThreads) {
-    const int m = i / nrows;
-    const int n = strip0 * 16 + (i - m * nrows);
-    // Issue every split's load before summing (one memory round trip), then
-    // add in split order.
-    float part[kMaxSplits];
+// One workgroup per row: the largest key over the GEMV's slots[m][0..G),
+// decoded to its column (lowest column among equal values, see argmax_key).
+// Each thread keeps four independent maxima over 16-byte loads, so its loads
+// are all in flight together; then a tree over the workgroup.
+constexpr int kFinishThreads = 1024;
+__global__ __launch_bounds__(kFinishThreads) void argmax_finish_kernel(
+    const unsigned long long* slots, int G, int32_t* index) {
+  __shared__ unsigned long long best[kFinishThreads];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const unsigned long long* row = slots + (int64_t)m * G;
+  unsigned long long k[4] = {0, 0, 0, 0};
+  // G * 8 bytes per row: the row starts 16-byte aligned when m * G is even.
+  const int lead = ((m * G) & 1) ? 1 : 0;
+  if (lead && tid == 0) k[0] = row[0];
+  const int pairs = (G - lead) / 2;
+  const ulonglong2* row2 = reinterpret_cast<const ulonglong2*>(row + lead);
+  int i = tid;
+#pragma unroll 1
+  for (; i + 3 * kFinishThreads < pairs; i += 4 * kFinishThreads) {
 #pragma unroll
-    for (int sp = 0; sp < kMaxSplits; ++sp)
-      part[sp] = sp < a.splits
-                     ? load_coherent(&a.partial[((int64_t)sp * a.M + m) * a.np + P_col0 + n])
-                     : 0.f;
-    float sum = part[0];
-#pragma unroll
-    for (int sp = 1; sp < kMaxSplits; ++sp)
-      if (sp < a.splits) sum += part[sp];
-    if (n < P_N) {
-      const float sc = (float)P_scale[n];
-      const float bi = P_bias ? (float)P_bias[n] : 0.f;
-      P_y[(int64_t)m * P_ldy + n] = (_Float16)__builtin_fmaf(sum, sc, bi);
+    for (int u = 0; u < 4; ++u) {
+      const ulonglong2 v = row2[i + u * kFinishThreads];
+      const unsigned long long w = v.x > v.y ? v.x : v.y;
+      k[u] = w > k[u] ? w : k[u];
     }
   }
-  if (tid == 0)
-    __hip_atomic_store(&a.counters[group], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (; i < pairs; i += kFinishThreads) {
+    const ulonglong2 v = row2[i];
+    const unsigned long long w = v.x > v.y ? v.x : v.y;
+    k[0] = w > k[0] ? w : k[0];
+  }
+  if (tid == 0 && lead + 2 * pairs < G) k[1] = row[G - 1] > k[1] ? row[G - 1] : k[1];
+  k[0] = k[0] > k[1] ? k[0] : k[1];
+  k[2] = k[2] > k[3] ? k[2] : k[3];
+  best[tid] = k[0] > k[2] ? k[0] : k[2];
+  __syncthreads();
+  for (int w = kFinishThreads / 2; w > 0; w >>= 1) {
+    if (tid < w && best[tid + w] > best[tid]) best[tid] = best[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) index[m] = argmax_index_of(best[0]);
 }
 
 template <int MT, int NS, int W, int U, bool XL, bool NT>
@@ -433,6 +533,7 @@ GemvKernelArgs make_args(const LinearProblem& pr, const GemvPlan& p, void* works
   ka.partial = workspace ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                     RF_W8A16_WS_COUNTER_BYTES)
                          : nullptr;
+  ka.amax_slots = nullptr;
   return ka;
 }
 
@@ -472,19 +573,7 @@ bool lds_fits(int cfg, int M, int kb_per_split) {
   return gemv_lds_bytes(d.mt, d.ns, d.w, d.xl, M, kb_per_split) <= 65536;
 }
 
-}  // namespace
-
-size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj) {
-  if (p.splits <= 1) return 0;
-  int64_t np = 0;
-  for (int i = 0; i < nproj; ++i) np += round_up(Ns[i], 16);
-  return (size_t)p.splits * (size_t)M * (size_t)np * sizeof(float);
-}
-
-hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspace,
-                       hipStream_t stream) {
-  if (pr.nproj < 1 || pr.nproj > kMaxProj) return hipErrorInvalidValue;
-  const GemvKernelArgs ka = make_args(pr, p, workspace);
+hipError_t launch_gemv_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t stream) {
   switch (p.cfg) {
     case kG1x1W16U4: return launch_t<1, 1, 16, 4, false, true>(ka, p, stream);
     case kG1x1W16U4XL: return launch_t<1, 1, 16, 4, true, true>(ka, p, stream);
@@ -503,6 +592,34 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
     default: return hipErrorInvalidValue;
   }
 }
+
+}  // namespace
+
+size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj) {
+  if (p.splits <= 1) return 0;
+  int64_t np = 0;
+  for (int i = 0; i < nproj; ++i) np += round_up(Ns[i], 16);
+  return (size_t)p.splits * (size_t)M * (size_t)np * sizeof(float);
+}
+
+hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspace,
+                       hipStream_t stream, const ArgmaxTarget* am) {
+  if (pr.nproj < 1 || pr.nproj > kMaxProj) return hipErrorInvalidValue;
+  GemvKernelArgs ka = make_args(pr, p, workspace);
+  if (am) {
+    if (pr.nproj != 1 || pr.M > 64 || !am->slots || !am->index) return hipErrorInvalidValue;
+    ka.amax_slots = reinterpret_cast<unsigned long long*>(am->slots);
+    const hipError_t e = launch_gemv_cfg(ka, p, stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(pr.M), dim3(kFinishThreads), 0, stream,
+                       static_cast<const unsigned long long*>(ka.amax_slots), p.groups, am->index);
+    return hipGetLastError();
+  }
+  return launch_gemv_cfg(ka, p, stream);
+}
+
+size_t argmax_slot_bytes(const GemvPlan& p, int M) { return (size_t)M * (size_t)p.groups * 8; }
+
 
 // Kernel choice per shape: the analogue of the reference's W8A16 tile
 // tables (src/ops/rpu_linear_tiling.h:69-127, selectors :544-595), but as

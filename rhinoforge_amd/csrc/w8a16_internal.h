@@ -66,9 +66,22 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
 size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj);
 size_t gemm_workspace_bytes(const GemmPlan& p);
 
+// Fused argmax of a single-projection GEMV launch (M <= 64): the GEMV
+// stores every workgroup's best 64-bit key per row to `slots` (scratch,
+// argmax_slot_bytes), a second launch reduces them into the int32 result.
+struct ArgmaxTarget {
+  uint64_t* slots;  // [M][groups]
+  int32_t* index;   // [M]
+};
+size_t argmax_slot_bytes(const GemvPlan& p, int M);
+
+// Split-K arrival counters (4 B per workgroup group or tile) fill the
+// zero-between-calls counter region at the start of every workspace.
+constexpr int kMaxSplitCounters = (int)(RF_W8A16_WS_COUNTER_BYTES / 4);
+
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspace,
-                       hipStream_t stream);
+                       hipStream_t stream, const ArgmaxTarget* am = nullptr);
 hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& p, void* workspace,
                        hipStream_t stream);
 hipError_t launch_pack(const int8_t* q, int64_t N, int64_t K, int64_t ldq,

@@ -248,6 +248,52 @@ at::Tensor linear_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
   no_cpu("w8a16::linear");
 }
 
+std::tuple<at::Tensor, at::Tensor> linear_argmax_cpu(const at::Tensor&, const at::Tensor&,
+                                                     const at::Tensor&,
+                                                     const c10::optional<at::Tensor>&, bool,
+                                                     int64_t) {
+  no_cpu("w8a16::linear_argmax");
+}
+
+// Greedy decode: the per-row argmax of the fp16 logits, folded into the GEMV
+// epilogue (M <= 64).  Returns (index int32 [...], logits fp16 [..., N] or an
+// empty tensor when return_logits is false).
+std::tuple<at::Tensor, at::Tensor> linear_argmax_hip(const at::Tensor& input,
+                                                     const at::Tensor& weight,
+                                                     const at::Tensor& scale,
+                                                     const c10::optional<at::Tensor>& bias,
+                                                     bool return_logits, int64_t layout) {
+  RECORD_FUNCTION("w8a16::linear_argmax", {});
+  const char* op = "w8a16::linear_argmax";
+  Checked c = check_args(input, weight, scale, bias, layout, op);
+  TORCH_CHECK(c.M <= 64, op, ": fused argmax covers decode batches of at most 64 rows, got M=",
+              c.M, " (use w8a16::linear and argmax for longer inputs)");
+  std::vector<int64_t> ishape = input.sizes().vec();
+  ishape.pop_back();
+  at::Tensor index = at::empty(ishape, input.options().dtype(at::kInt));
+  at::Tensor logits;
+  if (return_logits) {
+    std::vector<int64_t> lshape = input.sizes().vec();
+    lshape.back() = c.N;
+    logits = at::empty(lshape, input.options());
+  } else {
+    logits = at::empty({0}, input.options());
+  }
+  if (c.M == 0) return {index, logits};
+  c10::DeviceGuard dev_guard(c.x2.device());
+  void* stream = c10::hip::getCurrentHIPStream(c.x2.device().index()).stream();
+  const size_t ws_bytes = rf_w8a16_workspace_bytes_argmax(c.M, c.N, c.K);
+  TORCH_CHECK(ws_bytes > 0, op, ": ", rf_w8a16_status_str(RF_W8A16_EINVAL));
+  at::Tensor ws = workspace_cache().get(c.x2.device(), stream, ws_bytes);
+  const void* bptr = (bias.has_value() && bias->defined()) ? bias->data_ptr() : nullptr;
+  const int st = rf_w8a16_linear_argmax(
+      c.x2.data_ptr(), c.x2.stride(0), weight.data_ptr(), (int32_t)layout, scale.data_ptr(), bptr,
+      return_logits ? logits.data_ptr() : nullptr, c.N, index.data_ptr<int32_t>(), c.M, c.N, c.K,
+      ws.data_ptr(), (size_t)ws.numel(), stream);
+  check_status(st, op);
+  return {index, logits};
+}
+
 void linear_into_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
                      const c10::optional<at::Tensor>&, at::Tensor&, int64_t, int64_t) {
   no_cpu("w8a16::linear_into");
@@ -308,6 +354,8 @@ TORCH_LIBRARY(w8a16, m) {
         "Tensor(a!) out, int layout=1, int kernel=0) -> ()");
   m.def("linear_multi(Tensor input, Tensor[] weights, Tensor[] weight_scales, Tensor?[] biases, "
         "int layout=1, int kernel=0) -> Tensor[]");
+  m.def("linear_argmax(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias=None, "
+        "bool return_logits=False, int layout=1) -> (Tensor, Tensor)");
   m.def("pack_weight(Tensor q) -> Tensor", TORCH_FN(pack_weight));
   m.def("unpack_weight(Tensor packed, int N, int K) -> Tensor", TORCH_FN(unpack_weight));
   m.def("select_kernel(int M, int N, int K) -> int", TORCH_FN(select_kernel));
@@ -318,6 +366,7 @@ TORCH_LIBRARY_IMPL(w8a16, CUDA, m) {
   m.impl("linear", TORCH_FN(linear_hip));
   m.impl("linear_into", TORCH_FN(linear_into_hip));
   m.impl("linear_multi", TORCH_FN(linear_multi_hip));
+  m.impl("linear_argmax", TORCH_FN(linear_argmax_hip));
 }
 
 TORCH_LIBRARY_IMPL(w8a16, Meta, m) { m.impl("linear", TORCH_FN(linear_meta)); }
@@ -326,4 +375,5 @@ TORCH_LIBRARY_IMPL(w8a16, CPU, m) {
   m.impl("linear", TORCH_FN(linear_cpu));
   m.impl("linear_into", TORCH_FN(linear_into_cpu));
   m.impl("linear_multi", TORCH_FN(linear_multi_cpu));
+  m.impl("linear_argmax", TORCH_FN(linear_argmax_cpu));
 }

@@ -72,6 +72,24 @@ def linear_multi(input: torch.Tensor, weights, weight_scales, biases=None, *,
                                         layout, kernel)
 
 
+def linear_argmax(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                  bias=None, *, return_logits: bool = False, layout: int = LAYOUT_TILE16X64):
+    """Greedy-decode lm_head: the index of the largest fp16 logit per row.
+
+    Computes ``input . (s (.) q)^T (+ b)`` rounded to fp16 like ``linear`` and
+    returns its argmax over the last dimension as int32 (the lowest index
+    among equal maxima; NaN counts as the largest value, as torch.argmax
+    does), with the reduction folded into the decode GEMV's epilogue (at most
+    64 rows).  ``return_logits=True`` also returns the logits; otherwise
+    ``(index, empty tensor)``.  Replaces the reference's decode lm_head GEMM
+    followed by rpu_argmax (src/fused/rpu_qwen3_model.h:3653-3690,
+    src/ops/rpu_argmax.cpp:485-640).
+    """
+    index, logits = torch.ops.w8a16.linear_argmax(input, weight, weight_scale, bias,
+                                                  return_logits, layout)
+    return (index, logits) if return_logits else index
+
+
 def select_kernel(m: int, n: int, k: int) -> int:
     """Kernel the AUTO policy runs for (M, N, K): KERNEL_GEMV or KERNEL_GEMM."""
     return int(torch.ops.w8a16.select_kernel(m, n, k))

@@ -227,6 +227,135 @@ def test_cfg2_lm_head_argmax_agreement_1000_rows():
         assert len(bad) - ties == 0
 
 
+# ---------------------------------------------------------------- fused argmax (lm_head, greedy decode)
+def _argmax_first(y):
+    """Row argmax of fp16 logits, lowest index among equal values (torch.argmax's rule)."""
+    return y.float().argmax(-1).to(torch.int32)
+
+
+def _same_bits_or_nan(a, b):
+    """Bitwise equality where NaN positions must match (NaN compares unequal to itself)."""
+    return bool((a.isnan() == b.isnan()).all()) and torch.equal(a.nan_to_num(0.0), b.nan_to_num(0.0))
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_linear_argmax_cfg2_lm_head(m):
+    """cfg2 lm_head (151936 x 5120): the fused argmax equals the argmax of the op's own
+    fp16 logits exactly, and the logits it optionally returns are the linear op's, bit for bit."""
+    _say(f"linear_argmax cfg2 M={m}")
+    q_dev, s_dev = _lm_head_weights()
+    packed = rf.pack_weight(q_dev)
+    x = _to_dev(o.make_activation(o.derive_seed(2, "amax", m), m, 5120, rms_normalize=True))
+    idx = rf.linear_argmax(x, packed, s_dev)
+    idx2, logits = rf.linear_argmax(x, packed, s_dev, return_logits=True)
+    y = rf.linear(x, packed, s_dev)
+    torch.cuda.synchronize()
+    assert idx.dtype == torch.int32 and idx.shape == (m,)
+    assert torch.equal(logits, y)
+    assert torch.equal(idx, _argmax_first(y)), (idx, _argmax_first(y))
+    assert torch.equal(idx2, idx)
+
+
+def test_linear_argmax_agreement_1000_rows_with_cpu_path():
+    """Greedy-token agreement of the fused argmax (batches of 8 rows) with the reference
+    CPU path over 1000 seeded rows, with the same near-tie accounting as the logits test."""
+    _say("linear_argmax 1000 rows")
+    q_dev, s_dev = _lm_head_weights()
+    packed = rf.pack_weight(q_dev)
+    x = o.make_activation(o.derive_seed(2, "argmax"), 1000, 5120, rms_normalize=True)
+    xd = _to_dev(x)
+    a_gpu = torch.cat([rf.linear_argmax(xd[i:i + 8], packed, s_dev) for i in range(0, 1000, 8)])
+    torch.cuda.synchronize()
+    w16 = o.dequantize_fp32_then_fp16(q_dev.cpu().numpy(), s_dev.cpu().numpy())
+    y_cpu = (x.astype(np.float32) @ w16.astype(np.float32).T).astype(np.float16)
+    a_cpu = y_cpu.astype(np.float32).argmax(1)
+    a_gpu = a_gpu.cpu().numpy()
+    bad = np.nonzero(a_gpu != a_cpu)[0]
+    ties = sum(1 for r in bad if abs(float(y_cpu[r, a_cpu[r]]) - float(y_cpu[r, a_gpu[r]]))
+               <= 2 * float(np.spacing(np.float16(abs(float(y_cpu[r, a_cpu[r]]))))))
+    _say(f"  fused argmax: agree {1000 - len(bad)}/1000, near-ties {ties}")
+    assert len(bad) - ties == 0
+
+
+def test_linear_argmax_ties_nan_and_repeats():
+    """Equal maxima resolve to the lowest index; a NaN logit counts as the largest (torch.argmax's
+    rule); -0 equals +0; repeated calls (the workspace keys are reset) and a bias all agree with
+    argmax of the op's own logits."""
+    n, k = 700, 512
+    rng = np.random.default_rng(7)
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (rng.random(n) * 0.01 + 1e-3).astype(np.float16)
+    for dup in (650, 300, 5):  # identical channels: 5 must win over 300 and 650
+        q[dup] = q[123]
+        s[dup] = s[123]
+    s[[5, 123, 300, 650]] = np.float16(0.05)  # and make them the largest by far
+    packed, sd = rf.pack_weight(_to_dev(q)), _to_dev(s)
+    x = o.make_activation(31, 6, k)
+    x[:, :] = np.abs(x).astype(np.float16) * np.sign(q[123].astype(np.float32)).astype(np.float16)
+    x[3] = 0.0                 # all logits +0 (bias none): index 0
+    x[4, 7] = np.float16(np.nan)  # a NaN activation: every logit of row 4 is NaN -> index 0
+    x[5] = -x[5]               # row 5: channel 123's group is now the smallest; plain argmax
+    xd = _to_dev(x)
+    idx, y = rf.linear_argmax(xd, packed, sd, return_logits=True)
+    torch.cuda.synchronize()
+    assert idx[0].item() == 5 and idx[1].item() == 5 and idx[2].item() == 5
+    assert idx[3].item() == 0 and idx[4].item() == 0
+    assert torch.equal(idx, _argmax_first(y.nan_to_num(nan=float("inf"))))
+    b = _to_dev((o.normal(32, (n,)) * 0.1).astype(np.float16))
+    for _ in range(3):
+        i2, y2 = rf.linear_argmax(xd, packed, sd, b, return_logits=True)
+        i3 = rf.linear_argmax(xd, packed, sd)
+        torch.cuda.synchronize()
+        assert _same_bits_or_nan(y2, rf.linear(xd, packed, sd, b))
+        assert torch.equal(i2, _argmax_first(y2.nan_to_num(nan=float("inf"))))
+        assert torch.equal(i3, idx)
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 1000, 8192), (40, 3000, 1024), (64, 2000, 640), (3, 100, 136),
+                                   (1, 1000, 4096)])
+def test_linear_argmax_planner_paths(m, n, k):
+    """Split-K (the argmax runs in the last split's reduction), multi-row m-tiles, the
+    LDS-staged x configuration and a K tail: index == argmax of the op's own logits."""
+    _say(f"linear_argmax M={m} N={n} K={k}")
+    x, q, s, b = make_case(m, n, k, seed=33, bias=True)
+    packed = rf.pack_weight(_to_dev(q))
+    xd, sd, bd = _to_dev(x), _to_dev(s), _to_dev(b)
+    idx, y = rf.linear_argmax(xd, packed, sd, bd, return_logits=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y, rf.linear(xd, packed, sd, bd, kernel=rf.KERNEL_GEMV))
+    assert torch.equal(idx, _argmax_first(y))
+    assert_parity(y.cpu().numpy(), x, q, s, b, label=f"argmax logits {m}x{n}x{k}")
+
+
+def test_linear_argmax_capi_and_errors():
+    """The C ABI entry point through ctypes (no logits), and the op's refusals."""
+    m, n, k = 4, 5000, 1024
+    x, q, s, _ = make_case(m, n, k, seed=34)
+    packed = rf.pack_weight(_to_dev(q))
+    xd, sd = _to_dev(x), _to_dev(s)
+    lib = capi.load()
+    ws_bytes = lib.rf_w8a16_workspace_bytes_argmax(m, n, k)
+    assert ws_bytes > 0 and lib.rf_w8a16_workspace_bytes_argmax(65, n, k) == 0
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=DEV)
+    idx = torch.full((m,), -1, dtype=torch.int32, device=DEV)
+    for _ in range(2):
+        st = lib.rf_w8a16_linear_argmax(xd.data_ptr(), k, packed.data_ptr(), capi.LAYOUT_TILE16X64,
+                                        sd.data_ptr(), None, None, 0, idx.data_ptr(), m, n, k,
+                                        ws.data_ptr(), ws_bytes,
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        capi.check(st, "rf_w8a16_linear_argmax")
+        torch.cuda.synchronize()
+        assert torch.equal(idx, _argmax_first(rf.linear(xd, packed, sd)))
+        assert int(ws[:capi.WS_COUNTER_BYTES].count_nonzero()) == 0  # counters left zero
+    big = torch.zeros(65, k, dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError, match="at most 64 rows"):
+        rf.linear_argmax(big, packed, sd)
+    st = lib.rf_w8a16_linear_argmax(big.data_ptr(), k, packed.data_ptr(), capi.LAYOUT_TILE16X64,
+                                    sd.data_ptr(), None, None, 0, idx.data_ptr(), 65, n, k,
+                                    ws.data_ptr(), ws_bytes, None)
+    assert st == capi.EKERNEL
+
+
 # ---------------------------------------------------------------- edge cases
 EDGE = [(1, 1, 8), (1, 17, 72), (2, 100, 136), (16, 16, 64), (17, 33, 520), (33, 48, 1024),
         (64, 80, 200), (65, 33, 520), (3, 5, 4104), (200, 130, 264), (1, 4000, 16)]

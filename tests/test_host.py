@@ -152,6 +152,29 @@ def test_capi_linear_multi_validation_without_gpu():
     assert call(ok, 3) in (capi.EHIP, capi.EDEVICE)
 
 
+def test_capi_linear_argmax_validation_without_gpu():
+    lib = capi.load()
+    fake = 1 << 20
+
+    def call(M=1, N=1024, K=1024, ldx=1024, x=fake, w=fake, s=fake, y=None, ldy=0, idx=fake,
+             layout=capi.LAYOUT_TILE16X64):
+        return lib.rf_w8a16_linear_argmax(x, ldx, w, layout, s, None, y, ldy, idx, M, N, K,
+                                          None, 0, None)
+
+    assert call(idx=None) == capi.EINVAL
+    assert call(x=None) == capi.EINVAL
+    assert call(M=0) == capi.EINVAL
+    assert call(y=fake, ldy=100) == capi.EINVAL
+    assert call(layout=capi.LAYOUT_ROWMAJOR) == capi.ELAYOUT
+    assert call(idx=fake + 2) == capi.EALIGN
+    assert call(x=fake + 8) == capi.EALIGN
+    assert call(M=65) == capi.EKERNEL
+    assert call() in (capi.EHIP, capi.EDEVICE)
+    assert lib.rf_w8a16_workspace_bytes_argmax(64, 151936, 5120) >= capi.WS_COUNTER_BYTES
+    assert lib.rf_w8a16_workspace_bytes_argmax(65, 151936, 5120) == 0
+    assert lib.rf_w8a16_workspace_bytes_argmax(0, 16, 16) == 0
+
+
 def test_workspace_bytes_multi_matches_single():
     lib = capi.load()
     for m, n, k in [(1, 1024, 4096), (16, 4096, 12288), (9, 1000, 1024), (2048, 4096, 4096)]:
@@ -182,8 +205,8 @@ def test_workspace_bytes_counter_region():
 
 # ---------------------------------------------------------------- torch op
 def test_torch_op_schemas_registered():
-    for name in ("linear", "linear_into", "linear_multi", "pack_weight", "unpack_weight",
-                 "select_kernel"):
+    for name in ("linear", "linear_into", "linear_multi", "linear_argmax", "pack_weight",
+                 "unpack_weight", "select_kernel"):
         assert hasattr(torch.ops.w8a16, name)
 
 
@@ -208,6 +231,8 @@ def test_torch_op_refuses_cpu_tensors():
         rf.linear_into(x, w, s, None, torch.empty(2, 48, dtype=torch.float16))
     with pytest.raises(RuntimeError, match="no CPU implementation"):
         rf.linear_multi(x, [w, w], [s, s])
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        rf.linear_argmax(x, w, s)
 
 
 @pytest.mark.parametrize("bad", ["x_dtype", "w_dtype", "s_dtype", "layout"])
