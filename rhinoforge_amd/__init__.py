@@ -44,7 +44,7 @@ from .ops import (  # noqa: E402
     unpack_weight,
 )
 from .quant import dequantize_linear_per_channel, quantize_linear_per_channel  # noqa: E402
-from .nn import W8A16Linear  # noqa: E402
+from .nn import W8A16Embedding, W8A16Linear  # noqa: E402
 
 __all__ = [
     "LAYOUT_ROWMAJOR",
@@ -52,6 +52,7 @@ __all__ = [
     "KERNEL_AUTO",
     "KERNEL_GEMM",
     "KERNEL_GEMV",
+    "W8A16Embedding",
     "W8A16Linear",
     "dequantize_linear_per_channel",
     "linear",

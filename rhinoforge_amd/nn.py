@@ -39,20 +39,27 @@ class W8A16Linear(nn.Module):
 
     @classmethod
     def from_quantized(cls, q: torch.Tensor, weight_scale: torch.Tensor,
-                       bias: torch.Tensor | None = None) -> "W8A16Linear":
+                       bias: torch.Tensor | None = None, *, device=None) -> "W8A16Linear":
         """From an on-disk pair: ``X.weight`` int8 [N, K] row-major and
-        ``X.weight_scale`` fp16 [N] (quant/convert_qwen3.py:65-100 format)."""
+        ``X.weight_scale`` fp16 [N] (quant/convert_qwen3.py:65-100 format).
+
+        The weight is packed where it ends up: on ``device`` (default: q's
+        device) by the pack kernel for a HIP device, on the host for the CPU.
+        """
         if q.dtype != torch.int8 or q.dim() != 2:
             raise TypeError(f"weight must be int8 [N, K], got {q.dtype} {tuple(q.shape)}")
         n, k = q.shape
         if weight_scale.dtype != torch.float16 or tuple(weight_scale.shape) != (n,):
             raise TypeError(f"weight_scale must be fp16 [{n}], got {weight_scale.dtype} "
                             f"{tuple(weight_scale.shape)}")
+        if bias is not None and tuple(bias.shape) != (n,):
+            raise ValueError(f"bias must have shape ({n},), got {tuple(bias.shape)}")
+        device = torch.device(device) if device is not None else q.device
         mod = cls(k, n, bias=bias is not None, device="meta")
-        mod.weight = ops.pack_weight(q)
-        mod.weight_scale = weight_scale.contiguous()
+        mod.weight = ops.pack_weight(q.to(device))
+        mod.weight_scale = weight_scale.to(device).contiguous()
         if bias is not None:
-            mod.bias = bias.to(torch.float16).contiguous()
+            mod.bias = bias.to(device=device, dtype=torch.float16).contiguous()
         return mod
 
     @classmethod
@@ -72,3 +79,36 @@ class W8A16Linear(nn.Module):
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"bias={self.bias is not None}, layout=TILE16X64")
+
+
+class W8A16Embedding(nn.Module):
+    """Token embedding with an int8 row-major table and one fp16 scale per row.
+
+    The checkpoint form of ``quantized_embed_tokens`` (quant/load.py:303-316,
+    343-356): ``weight`` int8 [V, H], ``weight_scale`` fp16 [V].  A lookup
+    gathers rows and dequantizes them as ``fp16(f32(q) * f32(s))``
+    (adapters/qwen3.py:654-680); the table is gathered, never multiplied, so
+    it stays row-major.
+    """
+
+    def __init__(self, weight: torch.Tensor, weight_scale: torch.Tensor,
+                 padding_idx: int | None = None) -> None:
+        super().__init__()
+        if weight.dtype != torch.int8 or weight.dim() != 2:
+            raise TypeError(f"weight must be int8 [V, H], got {weight.dtype} "
+                            f"{tuple(weight.shape)}")
+        if weight_scale.dtype != torch.float16 or tuple(weight_scale.shape) != (weight.size(0),):
+            raise TypeError(f"weight_scale must be fp16 [{weight.size(0)}], got "
+                            f"{weight_scale.dtype} {tuple(weight_scale.shape)}")
+        self.num_embeddings, self.embedding_dim = weight.shape
+        self.padding_idx = padding_idx
+        self.register_buffer("weight", weight.contiguous())
+        self.register_buffer("weight_scale", weight_scale.contiguous())
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        rows = self.weight[input_ids].to(torch.float32)
+        return (rows * self.weight_scale[input_ids].to(torch.float32).unsqueeze(-1)
+                ).to(torch.float16)
+
+    def extra_repr(self) -> str:
+        return f"{self.num_embeddings}, {self.embedding_dim}, int8 rows"
