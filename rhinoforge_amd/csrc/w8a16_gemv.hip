@@ -540,7 +540,7 @@ GemvKernelArgs make_args(const LinearProblem& pr, const GemvPlan& p, void* works
 // Kernel configurations the planner chooses from (all stream weights with
 // non-temporal loads).  Measured on MI355X over the BASELINE decode shapes.
 enum GemvCfgId {
-  kG1x1W16U4,    // MT=1 NS=1 W=16 U=4
+  kG1x1W16U2,    // MT=1 NS=1 W=16 U=2  (U=4 without LDS staging spills at 128 VGPRs)
   kG1x1W16U4XL,  // MT=1 NS=1 W=16 U=4, x staged in LDS (M = 1, short K)
   kG1x1W8U4,     // MT=1 NS=1 W=8  U=4   (long K)
   kG1x1W8U4XL,   // MT=1 NS=1 W=8  U=4, x staged in LDS (many strips / long K)
@@ -575,7 +575,7 @@ bool lds_fits(int cfg, int M, int kb_per_split) {
 
 hipError_t launch_gemv_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t stream) {
   switch (p.cfg) {
-    case kG1x1W16U4: return launch_t<1, 1, 16, 4, false, true>(ka, p, stream);
+    case kG1x1W16U2: return launch_t<1, 1, 16, 2, false, true>(ka, p, stream);
     case kG1x1W16U4XL: return launch_t<1, 1, 16, 4, true, true>(ka, p, stream);
     case kG1x1W8U4: return launch_t<1, 1, 8, 4, false, true>(ka, p, stream);
     case kG1x1W8U4XL: return launch_t<1, 1, 8, 4, true, true>(ka, p, stream);
@@ -653,7 +653,7 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     } else {
       // (short K: one tile per wavefront does not amortize the staging wait)
       cfg = (M == 1 && kblocks >= 48 && lds_fits(kG1x1W16U4XL, M, kblocks)) ? kG1x1W16U4XL
-                                                                             : kG1x1W16U4;
+                                                                             : kG1x1W16U2;
     }
   } else if (M <= 16) {
     if (strips_ge(2048)) {
@@ -671,7 +671,7 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
       cfg = kG1x2W16U2;
       splits = 4;
     } else {
-      cfg = kG1x1W16U4;
+      cfg = kG1x1W16U2;
     }
   } else if (M <= 32) {
     if (strips_ge(1024)) {

@@ -281,3 +281,33 @@ def test_w8a16_linear_module_construction_on_cpu():
     assert torch.equal(mod.rowmajor_weight(), q) and torch.equal(mod.weight_scale, s)
     with pytest.raises(RuntimeError, match="no CPU implementation"):
         mod(torch.zeros(1, 128, dtype=torch.float16))
+
+
+def test_kernels_spill_nothing_to_scratch(tmp_path):
+    """Every gfx950 kernel fits its register budget: a spill to scratch memory
+    turns a bandwidth-bound kernel into one waiting on scratch traffic (the
+    compiler's resource-usage remarks, same flags as the product build)."""
+    import shutil
+    import subprocess
+    from rhinoforge_amd import _build
+
+    if shutil.which(_build.HIPCC) is None and not Path(_build.HIPCC).exists():
+        pytest.skip("hipcc not available")
+    srcs = sorted((ROOT / "rhinoforge_amd" / "csrc").glob("*.hip"))
+    procs = [(src, subprocess.Popen(
+        [_build.HIPCC, *_build.HIP_FLAGS, "-c", str(src), "-o", str(tmp_path / (src.stem + ".o")),
+         "-Rpass-analysis=kernel-resource-usage"],
+        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)) for src in srcs]
+    kernels = 0
+    for src, p in procs:
+        out, _ = p.communicate(timeout=600)
+        assert p.returncode == 0, out[-2000:]
+        name = None
+        for line in out.splitlines():
+            m = re.search(r"Function Name: (\S+)", line)
+            if m:
+                name, kernels = m.group(1), kernels + 1
+            m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+            if m:
+                assert int(m.group(1)) == 0, f"{src.name}: {name} uses {m.group(1)} B/lane scratch"
+    assert kernels >= 20
