@@ -358,7 +358,60 @@ def bench_other_configs(torch, rf):
     out["cfg4_vl32b"] = rows
     del copies
     torch.cuda.empty_cache()
+    out["w4a16"] = bench_w4a16(torch, rf)
     return out
+
+
+def nbytes_w4(m, n, k, gs):
+    """Algorithmic bytes of one W4A16 call: int4 weight, scales, x, y."""
+    scale = 2 * n * (k // gs if gs else 1)
+    return n * k // 2 + scale + 2 * m * k + 2 * m * n
+
+
+def bench_w4a16(torch, rf):
+    """W4A16 on the same Qwen3-8B shapes: decode projections at M 1 and 16 and the
+    M=2048 MLP prefill, per-channel and group-wise (32, 128); random int4 values
+    and scales, four rotated layer copies (384 MB, past the Infinity Cache)."""
+    rows = []
+    for gs in (0, 32, 128):
+        copies = []
+        for c in range(LAYER_COPIES):
+            g = torch.Generator(device="cuda").manual_seed(7000 + 10 * gs + c)
+            layer = []
+            for name, n, k in QWEN3_8B:
+                q = torch.randint(-8, 8, (n, k), generator=g, device="cuda", dtype=torch.int8)
+                sshape = (k // gs, n) if gs else (n,)
+                sc = (torch.rand(sshape, generator=g, device="cuda") * 0.01 + 1e-3).half()
+                layer.append((name, n, k, rf.pack_weight_int4(q), sc))
+                del q
+            copies.append(layer)
+        for m in (1, 16):
+            x = torch.randn(m, 12288, device="cuda").half()
+            step_bytes, step_us = 0, 0.0
+            for idx, (name, n, k) in enumerate(QWEN3_8B):
+                xx = x[:, :k]
+                us = per_launch_us(torch, lambda c: rf.linear_w4a16(xx, c[3], c[4]),
+                                   [layer[idx] for layer in copies], 40)
+                b = nbytes_w4(m, n, k, gs)
+                step_bytes, step_us = step_bytes + b, step_us + us
+                rows.append({"group_size": gs, "M": m, "proj": name, "N": n, "K": k,
+                             "us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1)})
+            rows.append({"group_size": gs, "M": m, "proj": "layer (7 launches)",
+                         "us": round(step_us, 2),
+                         "GBps": round(step_bytes / (step_us * 1e-6) / 1e9, 1)})
+        if gs in (0, 32):
+            x = torch.randn(PREFILL_M, 12288, device="cuda").half()
+            for idx in (4, 6):  # gate (12288x4096) and down (4096x12288)
+                name, n, k = QWEN3_8B[idx]
+                xx = x[:, :k]
+                us = per_launch_us(torch, lambda c: rf.linear_w4a16(xx, c[3], c[4]),
+                                   [layer[idx] for layer in copies], 6)
+                rows.append({"group_size": gs, "M": PREFILL_M, "proj": name, "N": n, "K": k,
+                             "us": round(us, 1),
+                             "TFLOPs": round(2 * PREFILL_M * n * k / (us * 1e-6) / 1e12, 1)})
+        del copies
+        torch.cuda.empty_cache()
+    return rows
 
 
 def cpu_baseline(budget_s=12.0):

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define RF_W8A16_ABI_VERSION 1
+#define RF_W8A16_ABI_VERSION 2
 
 /* Status codes.  The torch op maps each to a RuntimeError with the message
  * from rf_w8a16_status_str (the reference raises TORCH_CHECK before any
@@ -175,6 +175,59 @@ int rf_w8a16_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int
                            int32_t* index, int64_t M, int64_t N, int64_t K, void* workspace,
                            size_t workspace_bytes, void* stream);
 size_t rf_w8a16_workspace_bytes_argmax(int64_t M, int64_t N, int64_t K);
+
+/* ---------------------------------------------------------------------------
+ * W4A16: packed int4 weights, per-channel or group-wise fp16 scales, on the
+ * same two kernel families.  Replaces the reference's packed-int4 branch of
+ * the launcher (src/ops/rpu_linear.cpp:1211-1489: a uint8 [N, K/2] weight;
+ * a 1-D scale [N] selects per-channel, a 2-D scale the group-wise "pgrp"
+ * family) and its packers (python/rpu_backend/quant/int4_pack.py:21-58,
+ * int4_pgrp_pack.py:33-162).
+ *
+ * Operation:  y[M,N] = x[M,K] . W^T (+ b[N]), fp32 accumulation, with
+ *   per-channel (group_size 0):  W[n][k] = s[n] * q[n][k]   (s applied to the
+ *                                fp32 sum, as in the int8 path)
+ *   group-wise (32, 64 or 128):  W[n][k] = RN_fp16(s[k / group_size][n] * q[n][k])
+ *                                (the reference's fp16 dequantization,
+ *                                int4_pgrp_pack.py:63-70)
+ *   q[n][k] in [-8, 7] (int8 containers, quant/int4_pgrp_pack.py:33-60);
+ *   s fp16: [N], or [K/group_size][N] row-major (N contiguous) -- the logical
+ *   scale of int4_pgrp_pack.py:59, not the RPU's controller-striped payload.
+ *
+ * Shape rules, as the reference's int4 packers require (int4_pack.py:31-40,
+ * convert_qwen3_w4a16.py:65-76): N % 16 == 0, K % 64 == 0, and
+ * K % group_size == 0.
+ *
+ * RF_W8A16_LAYOUT_TILE16X128_I4: with Np = ceil(N/16)*16 and
+ *   Kp = ceil(K/128)*128 the buffer holds Np*Kp/2 bytes as 1024-byte tiles of
+ *   16 channels x 128 positions, tile (nb, kt) at byte offset
+ *   (nb*(Kp/128) + kt)*1024.  The 16 bytes at offset 16*l hold channel
+ *   16*nb + l%16, positions 128*kt + 32*(l/16) + 8*j + i (dword j = 0..3 of
+ *   the 16 bytes, i = 0..7); position i of a dword sits in nibble i/2 if i is
+ *   even and nibble 4 + i/2 if odd, as u = q + 8 (0..15).  Padding holds
+ *   q = 0.  Lane l of a wavefront loads exactly its four MFMA operands. */
+#define RF_W8A16_LAYOUT_TILE16X128_I4 2
+
+/* Bytes of a packed int4 weight (0 on bad sizes). */
+size_t rf_w4a16_packed_bytes(int64_t N, int64_t K);
+/* Host pack of q[N,K] (row stride ldq, values in [-8, 7]; others: EINVAL). */
+int rf_w4a16_pack_weight(const int8_t* q, int64_t N, int64_t K, int64_t ldq, void* dst,
+                         size_t dst_bytes);
+/* Inverse of rf_w4a16_pack_weight (host). */
+int rf_w4a16_unpack_weight(const void* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq);
+/* Device pack (device pointers, async on `stream`); values are taken mod 16
+ * as two's-complement nibbles, so only [-8, 7] round-trips. */
+int rf_w4a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K, int64_t ldq,
+                                void* dst_dev, size_t dst_bytes, void* stream);
+/* Workspace a W4A16 call needs (counter region + split-K partials). */
+size_t rf_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
+/* y = x . W^T (+ b) with a TILE16X128_I4 weight.  group_size: 0 (per-channel
+ * scale [N]) or 32 / 64 / 128 (scale [K/group_size][N], 16-byte aligned).
+ * kernel, workspace and stream as for rf_w8a16_linear. */
+int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void* scale,
+                    int32_t group_size, const void* bias, void* y, int64_t ldy, int64_t M,
+                    int64_t N, int64_t K, int32_t kernel, void* workspace, size_t workspace_bytes,
+                    void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

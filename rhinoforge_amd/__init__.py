@@ -34,17 +34,24 @@ from .ops import (  # noqa: E402
     KERNEL_AUTO,
     KERNEL_GEMM,
     KERNEL_GEMV,
+    LAYOUT_TILE16X128_I4,
     linear,
     linear_argmax,
     linear_into,
     linear_multi,
+    linear_w4a16,
     pack_weight,
+    pack_weight_int4,
     packed_shape,
+    packed_shape_int4,
     select_kernel,
     unpack_weight,
+    unpack_weight_int4,
 )
-from .quant import dequantize_linear_per_channel, quantize_linear_per_channel  # noqa: E402
-from .nn import W8A16Embedding, W8A16Linear  # noqa: E402
+from .quant import (dequantize_int4_group_wise, dequantize_linear_per_channel,  # noqa: E402
+                    quantize_int4_group_wise, quantize_int4_per_channel,
+                    quantize_linear_per_channel)
+from .nn import W4A16Linear, W8A16Embedding, W8A16Linear  # noqa: E402
 
 __all__ = [
     "LAYOUT_ROWMAJOR",
@@ -52,16 +59,25 @@ __all__ = [
     "KERNEL_AUTO",
     "KERNEL_GEMM",
     "KERNEL_GEMV",
+    "LAYOUT_TILE16X128_I4",
+    "W4A16Linear",
     "W8A16Embedding",
     "W8A16Linear",
+    "dequantize_int4_group_wise",
     "dequantize_linear_per_channel",
     "linear",
     "linear_argmax",
     "linear_into",
     "linear_multi",
+    "linear_w4a16",
     "pack_weight",
+    "pack_weight_int4",
     "packed_shape",
+    "packed_shape_int4",
+    "quantize_int4_group_wise",
+    "quantize_int4_per_channel",
     "quantize_linear_per_channel",
     "select_kernel",
     "unpack_weight",
+    "unpack_weight_int4",
 ]

@@ -63,6 +63,18 @@ SIGNATURES = {
                                           _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                           _c.c_void_p, _c.c_size_t, _c.c_void_p]),
     "rf_w8a16_workspace_bytes_argmax": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int64]),
+    "rf_w4a16_packed_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64]),
+    "rf_w4a16_pack_weight": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
+                                        _c.c_void_p, _c.c_size_t]),
+    "rf_w4a16_unpack_weight": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p,
+                                          _c.c_int64]),
+    "rf_w4a16_pack_weight_device": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
+                                               _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "rf_w4a16_workspace_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int64]),
+    "rf_w4a16_linear": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_void_p,
+                                   _c.c_int32, _c.c_void_p, _c.c_void_p, _c.c_int64,
+                                   _c.c_int64, _c.c_int64, _c.c_int64, _c.c_int32,
+                                   _c.c_void_p, _c.c_size_t, _c.c_void_p]),
 }
 
 _lib = None

@@ -75,6 +75,46 @@ __global__ void pack_kernel(const int8_t* __restrict__ q, int64_t N, int64_t K, 
 }
 }  // namespace
 
+// Int4 (TILE16X128_I4): nibble of position i (0..7) inside a dword.
+__host__ __device__ inline int i4_nibble(int i) { return (i & 1) ? 4 + (i >> 1) : (i >> 1); }
+
+namespace {
+__global__ void pack4_kernel(const int8_t* __restrict__ q, int64_t N, int64_t K, int64_t ldq,
+                             uint8_t* __restrict__ dst, int64_t ktiles, int64_t chunks) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= chunks) return;
+  const int64_t tile = idx >> 6;
+  const int lane = (int)(idx & 63);
+  const int64_t nb = tile / ktiles, kt = tile % ktiles;
+  const int64_t n = nb * 16 + (lane & 15);
+  const int64_t k0 = kt * 128 + 32 * (lane >> 4);
+  uint32_t words[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t k = k0 + 8 * w + i;
+      const int qv = (n < N && k < K) ? (int)q[n * ldq + k] : 0;
+      v |= (uint32_t)((qv + 8) & 0xF) << (4 * i4_nibble(i));
+    }
+    words[w] = v;
+  }
+  *reinterpret_cast<uint4*>(dst + idx * 16) = make_uint4(words[0], words[1], words[2], words[3]);
+}
+}  // namespace
+
+hipError_t launch_pack4(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* dst,
+                        hipStream_t stream) {
+  const int64_t ktiles = ceil_div(K, 128);
+  const int64_t chunks = ceil_div(N, 16) * ktiles * 64;
+  const int64_t blocks = ceil_div(chunks, 256);
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pack4_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, q, N, K, ldq, dst,
+                     ktiles, chunks);
+  return hipGetLastError();
+}
+
 hipError_t launch_pack(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* dst,
                        hipStream_t stream) {
   const int64_t kblocks = ceil_div(K, 64);
@@ -291,6 +331,143 @@ int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed, int32_t la
   q.N = N;
   return rf_w8a16_linear_multi(x, ldx, layout, &q, 1, M, K, kernel, workspace, workspace_bytes,
                                stream);
+}
+
+// ---------------------------------------------------------------------------
+// W4A16
+// ---------------------------------------------------------------------------
+size_t rf_w4a16_packed_bytes(int64_t N, int64_t K) {
+  if (check_nk(N, K) != RF_W8A16_OK) return 0;
+  return (size_t)round_up(N, 16) * (size_t)round_up(K, 128) / 2;
+}
+
+int rf_w4a16_pack_weight(const int8_t* q, int64_t N, int64_t K, int64_t ldq, void* dst,
+                         size_t dst_bytes) {
+  if (check_nk(N, K) != RF_W8A16_OK || !q || !dst || ldq < K) return RF_W8A16_EINVAL;
+  if (dst_bytes < rf_w4a16_packed_bytes(N, K)) return RF_W8A16_EINVAL;
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t k = 0; k < K; ++k)
+      if (q[n * ldq + k] < -8 || q[n * ldq + k] > 7) return RF_W8A16_EINVAL;
+  const int64_t ktiles = ceil_div(K, 128), nstrips = ceil_div(N, 16);
+  uint8_t* out = static_cast<uint8_t*>(dst);
+  for (int64_t nb = 0; nb < nstrips; ++nb)
+    for (int64_t kt = 0; kt < ktiles; ++kt) {
+      uint8_t* tile = out + (nb * ktiles + kt) * 1024;
+      for (int l = 0; l < 64; ++l) {
+        const int64_t n = nb * 16 + (l & 15);
+        for (int w = 0; w < 4; ++w) {
+          uint32_t v = 0;
+          for (int i = 0; i < 8; ++i) {
+            const int64_t k = kt * 128 + 32 * (l >> 4) + 8 * w + i;
+            const int qv = (n < N && k < K) ? (int)q[n * ldq + k] : 0;
+            v |= (uint32_t)(qv + 8) << (4 * rf::i4_nibble(i));
+          }
+          memcpy(tile + l * 16 + 4 * w, &v, 4);  // little-endian dword
+        }
+      }
+    }
+  return RF_W8A16_OK;
+}
+
+int rf_w4a16_unpack_weight(const void* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq) {
+  if (check_nk(N, K) != RF_W8A16_OK || !packed || !q || ldq < K) return RF_W8A16_EINVAL;
+  const int64_t ktiles = ceil_div(K, 128);
+  const uint8_t* in = static_cast<const uint8_t*>(packed);
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t k = 0; k < K; ++k) {
+      const int64_t kt = k >> 7;
+      const int kk = (int)(k & 127);
+      const int l = (int)(n & 15) + 16 * (kk >> 5), w = (kk >> 3) & 3, i = kk & 7;
+      uint32_t v;
+      memcpy(&v, in + ((n >> 4) * ktiles + kt) * 1024 + l * 16 + 4 * w, 4);
+      q[n * ldq + k] = (int8_t)((int)((v >> (4 * rf::i4_nibble(i))) & 0xF) - 8);
+    }
+  return RF_W8A16_OK;
+}
+
+int rf_w4a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K, int64_t ldq,
+                                void* dst_dev, size_t dst_bytes, void* stream) {
+  if (check_nk(N, K) != RF_W8A16_OK || !q_dev || !dst_dev || ldq < K) return RF_W8A16_EINVAL;
+  if (dst_bytes < rf_w4a16_packed_bytes(N, K)) return RF_W8A16_EINVAL;
+  if (!aligned(dst_dev, 16)) return RF_W8A16_EALIGN;
+  hipError_t e = rf::launch_pack4(q_dev, N, K, ldq, static_cast<uint8_t*>(dst_dev),
+                                  static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
+}
+
+size_t rf_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return 0;
+  rf::DeviceInfo dev;
+  if (rf::device_info(&dev) != RF_W8A16_OK) {
+    dev.cus = 256;
+    dev.gfx950 = false;
+  }
+  const int n32 = (int)N;
+  size_t extra = rf::gemm_workspace_bytes(rf::plan_gemm((int)M, &n32, 1, (int)K, dev));
+  if (M <= 64) {
+    const rf::GemvPlan p = rf::plan_gemv_int4((int)M, n32, (int)K, dev);
+    const size_t g = rf::gemv_workspace_bytes(p, (int)M, &n32, 1);
+    extra = g > extra ? g : extra;
+  }
+  return RF_W8A16_WS_COUNTER_BYTES + extra;
+}
+
+int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void* scale,
+                    int32_t group_size, const void* bias, void* y, int64_t ldy, int64_t M,
+                    int64_t N, int64_t K, int32_t kernel, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  if (!x || !w_packed || !scale || !y) return RF_W8A16_EINVAL;
+  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK || ldx < K || ldy < N)
+    return RF_W8A16_EINVAL;
+  if (group_size != 0 && group_size != 32 && group_size != 64 && group_size != 128)
+    return RF_W8A16_EINVAL;
+  if (N % 16 != 0 || K % 64 != 0 || (group_size && K % group_size != 0)) return RF_W8A16_EINVAL;
+  if (ldx % 8 != 0 || !aligned(x, 16) || !aligned(w_packed, 16) ||
+      !aligned(scale, group_size ? 16 : 2) || !aligned(y, 2) || (bias && !aligned(bias, 2)))
+    return RF_W8A16_EALIGN;
+
+  rf::DeviceInfo dev;
+  int st = rf::device_info(&dev);
+  if (st != RF_W8A16_OK) return st;
+  if (!dev.gfx950) return RF_W8A16_EDEVICE;
+
+  if (kernel == RF_W8A16_KERNEL_AUTO) kernel = auto_kernel(M);
+  if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
+  if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  rf::LinearProblem pr;
+  pr.x = static_cast<const _Float16*>(x);
+  pr.ldx = ldx;
+  pr.M = (int)M;
+  pr.K = (int)K;
+  pr.nproj = 1;
+  pr.wf = group_size ? rf::kWfInt4Grp : rf::kWfInt4;
+  pr.gshift = group_size == 128 ? 2 : group_size == 64 ? 1 : 0;
+  rf::Projection& d = pr.proj[0];
+  d.w = static_cast<const uint8_t*>(w_packed);
+  d.scale = static_cast<const _Float16*>(scale);
+  d.bias = static_cast<const _Float16*>(bias);
+  d.y = static_cast<_Float16*>(y);
+  d.ldy = ldy;
+  d.N = (int)N;
+  const int n32 = d.N;
+  auto workspace_ok = [&](size_t extra) {
+    return workspace && workspace_bytes >= RF_W8A16_WS_COUNTER_BYTES + extra &&
+           aligned(workspace, 256);
+  };
+  hipError_t e;
+  if (kernel == RF_W8A16_KERNEL_GEMV) {
+    const rf::GemvPlan p = rf::plan_gemv_int4(pr.M, n32, pr.K, dev);
+    if (p.splits > 1 && !workspace_ok(rf::gemv_workspace_bytes(p, pr.M, &n32, 1)))
+      return RF_W8A16_EWORKSPACE;
+    e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);
+  } else {
+    const rf::GemmPlan p = rf::plan_gemm(pr.M, &n32, 1, pr.K, dev);
+    if (p.splits > 1 && !workspace_ok(rf::gemm_workspace_bytes(p))) return RF_W8A16_EWORKSPACE;
+    e = rf::launch_gemm(pr, p, p.splits > 1 ? workspace : nullptr, s);
+  }
+  return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
 }
 
 size_t rf_w8a16_workspace_bytes_argmax(int64_t M, int64_t N, int64_t K) {

@@ -45,6 +45,62 @@ __device__ __forceinline__ half8 dequant8(uint32_t d0, uint32_t d1) {
   return __builtin_shufflevector(dequant4(d0), dequant4(d1), 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Packed int4 (TILE16X128_I4, include/w8a16.h): one tile = 16 output
+// channels x 128 input channels in 1024 bytes; lane l owns the 16 bytes at
+// 16*l: channel l%16, input positions 32*(l/16) .. +31 of the tile, as four
+// dwords of eight positions each.  Within a dword, nibble p (bits 4p..4p+3)
+// holds position 2p (p < 4) or 2(p-4)+1 (p >= 4), stored as u = q + 8.
+constexpr int kTileK4 = 128;
+
+// (a & m) | c in one VALU op.  CDNA3/4 VOP3 encodings take no literal
+// constants, so without this the compiler splits it into v_and + v_or.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+  return r;
+}
+
+// Exact int4 -> fp16 of one dword (eight positions, in position order), with
+// the magic-number conversion (Kim et al. 2022) applied to two nibbles per
+// fp16 pair:
+//   (d & 0x000F000F) | 0x64006400  = (1024 + u_lo, 1024 + u_hi) for nibbles
+//                                    p, p+4 at bits 0..3 of each half;
+//   (d & 0x00F000F0) | 0x64006400  = (1024 + 16 u, ...) for nibbles p+1, p+5;
+// subtracting 1032, or scaling by 1/16 and subtracting 72 (one fused op:
+// 64 + u - 72, all exact in fp16), gives q = u - 8; d >> 8 repeats this for
+// nibbles 2, 6 and 3, 7.  Nine VALU ops per eight weights.
+__device__ __forceinline__ half8 dequant8_i4(uint32_t d) {
+  const uint32_t e = 0x64006400u;
+  const uint32_t lo = and_or(d, 0x000F000Fu, e), hi = and_or(d, 0x00F000F0u, e);
+  const uint32_t d8 = d >> 8;
+  const uint32_t lo8 = and_or(d8, 0x000F000Fu, e), hi8 = and_or(d8, 0x00F000F0u, e);
+  const half2v off = {(_Float16)1032.0f, (_Float16)1032.0f};
+  const half2v k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const half2v b72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const half2v p0 = __builtin_bit_cast(half2v, lo) - off;                             // 0, 1
+  const half2v p1 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, hi), k16, b72);  // 2, 3
+  const half2v p2 = __builtin_bit_cast(half2v, lo8) - off;                            // 4, 5
+  const half2v p3 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, hi8), k16, b72); // 6, 7
+  return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3),
+                                 __builtin_shufflevector(p2, p3, 0, 1, 2, 3), 0, 1, 2, 3, 4, 5,
+                                 6, 7);
+}
+
+// The same with a group scale applied: RN_fp16(q * s) per weight (the
+// product of an integer |q| <= 8 and an fp16 scale, rounded once, as the
+// reference's fp16 dequantization computes it).
+__device__ __forceinline__ half8 dequant8_i4_scaled(uint32_t d, _Float16 s) {
+  const half8 sv = {s, s, s, s, s, s, s, s};
+  return dequant8_i4(d) * sv;
+}
+
+// Weight formats of a launch: the kernels are templated on it.
+enum WeightFormat : int {
+  kWfInt8 = 0,     // TILE16X64, per-channel scale [N] (epilogue)
+  kWfInt4 = 1,     // TILE16X128_I4, per-channel scale [N] (epilogue)
+  kWfInt4Grp = 2,  // TILE16X128_I4, group scale [K/gs][N] applied at dequant
+};
+
 // D(16x16, fp32) += A(16x32, fp16) * B(32x16, fp16).
 // Lane l supplies A row l%16 and B column l%16, each for the 8 K positions
 // of k-group l/16; the product pairs A and B slots with the same (group,

@@ -60,6 +60,8 @@ struct GemmKernelArgs {
   int kb_per_split;
   float* partial;        // [splits][tiles][BM*BN], fp32
   uint32_t* counters;    // [tiles], zero between calls
+  int wtiles;            // 1 KB weight tiles per strip along K (64 positions int8, 128 int4)
+  int gshift;            // group-wise int4: log2(group_size / 32)
 };
 
 // The weight matrix (and its tile column) behind global tile column tile_n.
@@ -140,7 +142,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(float* base, uint
 // fp32 epilogue: y = acc * scale[n] + bias[n].  Lane l holds
 // D[4*(l/16) + r][l%16] of each 16x16 tile; a full tile stores without
 // per-element checks.
-template <int TM, int TN>
+template <int TM, int TN, bool SC = true>
 __device__ __forceinline__ void store_tile(const TileTarget& t, const floatx4 (&acc)[TM][TN],
                                            int m0w, int n0w, int lane, int M, bool full) {
   const int nl = n0w + (lane & 15);
@@ -150,7 +152,7 @@ __device__ __forceinline__ void store_tile(const TileTarget& t, const floatx4 (&
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = nl + j * 16;
-    sc[j] = n < t.N ? (float)t.scale[n] : 0.f;
+    sc[j] = n < t.N ? (SC ? (float)t.scale[n] : 1.f) : 0.f;
     bi[j] = (t.bias && n < t.N) ? (float)t.bias[n] : 0.f;
   }
   if (full) {
@@ -189,7 +191,16 @@ __device__ __forceinline__ void store_tile(const TileTarget& t, const floatx4 (&
 // (valid) addresses; their results are never stored.  Columns past K (the
 // last K block when K % 64 != 0) are zeroed in LDS after their load lands.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
+//
+// WF (WeightFormat) int4: a 1 KB TILE16X128_I4 tile covers two K blocks; the
+// half for K block kb (lanes 32*(kb%2) .. +31 of the tile, 512 contiguous
+// bytes) is copied per strip, and lane (g = l/16, c = l%16) reads the eight
+// bytes holding positions 16g .. 16g+15 of the block for channel c: bytes
+// 8*(g%2) .. +7 of half-tile lane c + 16*(g/2), i.e. the two MFMA operands
+// of the int8 path (so the A operand path is shared unchanged).  Group-wise
+// int4 also copies the block's scale rows ([K/gs][N], BN columns; one row,
+// or two for gs = 32) into LDS, by wavefront 0, and scales at dequantization.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(OCC * WAVES_M * WAVES_N / 4, 8)))
 void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
@@ -197,8 +208,12 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   constexpr int TM = WM / 16, TN = WN / 16;
   constexpr int A_BYTES = BM * 128;
   constexpr int B_TILES = BN / 16;
-  constexpr int B_BYTES = B_TILES * kTileBytes;
-  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int B_STRIP = WF ? kTileBytes / 2 : kTileBytes;  // per strip and K block
+  constexpr int B_BYTES = B_TILES * B_STRIP;
+  constexpr bool GS = WF == kWfInt4Grp;
+  constexpr int S_BYTES = GS ? 1024 : 0;  // one wavefront DMA of scale rows
+  static_assert(!GS || 2 * BN * 2 <= S_BYTES, "two scale rows of BN fp16 fit one DMA");
+  constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
   constexpr int A_LOADS = A_BYTES / (NT * 16);
   constexpr int B_LOADS = B_BYTES / (NT * 16);
   constexpr int LOADS = A_LOADS + B_LOADS;
@@ -225,7 +240,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
 
   // Wave-uniform bases and per-lane 32-bit offsets.
   const uint8_t* abase = reinterpret_cast<const uint8_t*>(a.x + (int64_t)m0 * a.ldx);
-  const uint8_t* bbase = tt.w + (int64_t)strip0 * a.kblocks * kTileBytes;
+  const uint8_t* bbase = tt.w + (int64_t)strip0 * a.wtiles * kTileBytes;
   uint32_t aoff[A_LOADS], arow_off[A_LOADS];
   int acol[A_LOADS];
 #pragma unroll
@@ -241,8 +256,28 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   uint32_t boff[B_LOADS];
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
-    const int t = min(strip0 + wave * B_LOADS + i, tt.nstrips - 1) - strip0;
-    boff[i] = (uint32_t)t * (uint32_t)a.kblocks * kTileBytes + lane * 16;
+    if (WF) {
+      // 16-byte chunk p of the stage's B: strip p/32, chunk p%32 of its half tile
+      const int p = (wave * B_LOADS + i) * 64 + lane;
+      const int t = min(strip0 + (p >> 5), tt.nstrips - 1) - strip0;
+      boff[i] = (uint32_t)t * (uint32_t)a.wtiles * kTileBytes + (p & 31) * 16;
+    } else {
+      const int t = min(strip0 + wave * B_LOADS + i, tt.nstrips - 1) - strip0;
+      boff[i] = (uint32_t)t * (uint32_t)a.wtiles * kTileBytes + lane * 16;
+    }
+  }
+  // Group-wise int4 scale rows: chunk q = lane of row q / (BN/8) (lanes past
+  // the rows repeat the last chunk into the unused tail of the region);
+  // columns past N are clamped into the row (their outputs are not stored).
+  const _Float16* sbase = nullptr;
+  uint32_t soff = 0;
+  if (GS) {
+    const int gpb = a.gshift == 0 ? 2 : 1;  // scale rows per 64-wide K block
+    const int q = min(lane, gpb * (BN / 8) - 1);
+    const int r = q / (BN / 8), cc = q % (BN / 8);
+    const int n0 = strip0 * 16;
+    sbase = tt.scale + n0;
+    soff = (uint32_t)(r * tt.N * 2 + min(n0 * 2 + cc * 16, tt.N * 2 - 16) - n0 * 2);
   }
   const bool k_tail = (a.K & 63) != 0;
 
@@ -265,9 +300,12 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
 #pragma unroll
       for (int l = 0; l < A_LOADS; ++l) dma16s(aoff[l], ab, st + (wave_u * A_LOADS + l) * 1024);
     }
-    const uint8_t* bb = bbase + (int64_t)kb * kTileBytes;
+    const uint8_t* bb = bbase + (WF ? (int64_t)(kb >> 1) * kTileBytes + (kb & 1) * (kTileBytes / 2)
+                                    : (int64_t)kb * kTileBytes);
 #pragma unroll
     for (int l = 0; l < B_LOADS; ++l) dma16s(boff[l], bb, st + A_BYTES + (wave_u * B_LOADS + l) * 1024);
+    if (GS && wave_u == 0)
+      dma16s(soff, sbase + (int64_t)((2 * kb) >> a.gshift) * tt.N, st + A_BYTES + B_BYTES);
   };
   auto fix_tail = [&](int i) {
     const int kb = kb0 + i;
@@ -288,23 +326,52 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   const int sw = a_swizzle(arow);  // same for arow + 16*i
   const int aoff0 = arow * 128 + (((2 * (lane >> 4)) ^ sw) * 16);
   const int aoff1 = arow * 128 + (((2 * (lane >> 4) + 1) ^ sw) * 16);
+  // int4: half-tile lane and byte offset of this lane's eight bytes
+  const int b4off = ((lane & 15) + 16 * (lane >> 5)) * 16 + 8 * ((lane >> 4) & 1);
+  // group-wise: this lane's scale row in the block (gs = 32: positions 16g..16g+15
+  // lie in group g/2 of the block's two)
+  const int s4off = GS ? (((a.gshift == 0) ? (lane >> 5) : 0) * BN + wn * TN * 16 + (lane & 15)) * 2 : 0;
   auto compute = [&](int i) {
     const uint8_t* st = smem + (i % STAGES) * STAGE;
-    uint4 braw[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-      braw[j] = *reinterpret_cast<const uint4*>(st + A_BYTES + (wn * TN + j) * kTileBytes + lane * 16);
-#pragma unroll
-    for (int step = 0; step < 2; ++step) {
-      half8 af[TM];
-      const int ao = step == 0 ? aoff0 : aoff1;
-#pragma unroll
-      for (int r = 0; r < TM; ++r) af[r] = *reinterpret_cast<const half8*>(st + ao + r * 16 * 128);
+    if constexpr (WF != kWfInt8) {
+      uint2 braw[TN];
+      _Float16 sc[GS ? TN : 1];
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const half8 b = step == 0 ? dequant8(braw[j].x, braw[j].y) : dequant8(braw[j].z, braw[j].w);
+        braw[j] = *reinterpret_cast<const uint2*>(st + A_BYTES + (wn * TN + j) * B_STRIP + b4off);
+        if (GS) sc[GS ? j : 0] = *reinterpret_cast<const _Float16*>(st + A_BYTES + B_BYTES + s4off + j * 32);
+      }
 #pragma unroll
-        for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(af[r], b, acc[r][j]);
+      for (int step = 0; step < 2; ++step) {
+        half8 af[TM];
+        const int ao = step == 0 ? aoff0 : aoff1;
+#pragma unroll
+        for (int r = 0; r < TM; ++r) af[r] = *reinterpret_cast<const half8*>(st + ao + r * 16 * 128);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const uint32_t d = step == 0 ? braw[j].x : braw[j].y;
+          const half8 b = GS ? dequant8_i4_scaled(d, sc[GS ? j : 0]) : dequant8_i4(d);
+#pragma unroll
+          for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(af[r], b, acc[r][j]);
+        }
+      }
+    } else {
+      uint4 braw[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        braw[j] = *reinterpret_cast<const uint4*>(st + A_BYTES + (wn * TN + j) * kTileBytes + lane * 16);
+#pragma unroll
+      for (int step = 0; step < 2; ++step) {
+        half8 af[TM];
+        const int ao = step == 0 ? aoff0 : aoff1;
+#pragma unroll
+        for (int r = 0; r < TM; ++r) af[r] = *reinterpret_cast<const half8*>(st + ao + r * 16 * 128);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const half8 b = step == 0 ? dequant8(braw[j].x, braw[j].y) : dequant8(braw[j].z, braw[j].w);
+#pragma unroll
+          for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(af[r], b, acc[r][j]);
+        }
       }
     }
   };
@@ -312,11 +379,19 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < nk) issue(s);
+  // Group-wise int4: wavefront 0 issues one more DMA per K block (scale rows).
+  const bool extra = GS && wave_u == 0;
   for (int i = 0; i < nk; ++i) {
     const int ahead = min(STAGES - 2, nk - 1 - i);  // blocks issued after i
-    if (ahead >= 2) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LOADS) : "memory");
-    else if (ahead == 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS) : "memory");
-    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (ahead >= 2) {
+      if (extra) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (LOADS + 1)) : "memory");
+      else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LOADS) : "memory");
+    } else if (ahead == 1) {
+      if (extra) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS + 1) : "memory");
+      else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS) : "memory");
+    } else {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     if (k_tail && kb0 + i == a.kblocks - 1) fix_tail(i);
     barrier_lds();
     // Everyone is past compute(i-1): its stage can be refilled.
@@ -377,14 +452,14 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   }
 
   const bool full = m0 + BM <= a.M && (strip0 + B_TILES) * 16 <= tt.N;
-  store_tile<TM, TN>(tt, acc, m0 + wm * WM, (strip0 + wn * TN) * 16, lane, a.M, full);
+  store_tile<TM, TN, !GS>(tt, acc, m0 + wm * WM, (strip0 + wn * TN) * 16, lane, a.M, full);
 }
 
 // True when the 32-bit DMA offsets of w8a16_gemm_v3_kernel cannot overflow
 // for any projection of the launch.
 inline bool v3_offsets_fit(const GemmKernelArgs& ka, int bm, int bn) {
   const uint64_t a_span = (uint64_t)bm * (uint64_t)ka.ldx * 2 + (uint64_t)ka.kblocks * 128;
-  const uint64_t b_span = (uint64_t)(bn / 16) * (uint64_t)ka.kblocks * kTileBytes;
+  const uint64_t b_span = (uint64_t)(bn / 16) * (uint64_t)ka.wtiles * kTileBytes;
   return a_span < (1ull << 32) && b_span < (1ull << 32);
 }
 
@@ -438,7 +513,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
     const int strip = min(strip0 + wave * B_LOADS + i, tt.nstrips - 1);
-    bsrc[i] = tt.w + (int64_t)strip * a.kblocks * kTileBytes + lane * 16;
+    bsrc[i] = tt.w + (int64_t)strip * a.wtiles * kTileBytes + lane * 16;
   }
   const bool k_tail = (a.K & 63) != 0;
 
@@ -511,13 +586,13 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(
   store_tile<TM, TN>(tt, acc, m0 + wm * WM, (strip0 + wn * TN) * 16, lane, a.M, full);
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8>
 hipError_t launch_v3_t(const GemmKernelArgs& ka, hipStream_t stream) {
   const int64_t tiles = (int64_t)ka.tiles_m * ka.tiles_n;
   if (tiles <= 0 || tiles > 0x7fffffff || ka.splits < 1 || ka.splits > 65535 ||
       !v3_offsets_fit(ka, BM, BN))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC>),
+  hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, WF>),
                      dim3((unsigned)tiles, (unsigned)ka.splits), dim3(WAVES_M * WAVES_N * 64), 0,
                      stream, ka);
   return hipGetLastError();
@@ -550,6 +625,18 @@ constexpr int kGemmTile[kGemmCfgCount][3] = {{128, 256, 2}, {128, 128, 3}, {128,
                                              {64, 256, 2},  {256, 256, 1}, {128, 128, 1}};
 
 namespace {
+
+template <int WF>
+hipError_t launch_gemm4(int cfg, const GemmKernelArgs& ka, hipStream_t stream) {
+  switch (cfg) {
+    case kV3M128N256: return launch_v3_t<128, 256, 1, 4, 2, 2, WF>(ka, stream);
+    case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3, WF>(ka, stream);
+    case kV3M128N128S3: return launch_v3_t<128, 128, 1, 4, 3, 2, WF>(ka, stream);
+    case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2, WF>(ka, stream);
+    case kV3M256N256: return launch_v3_t<256, 256, 2, 4, 2, 1, WF>(ka, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 constexpr int kMaxGemmSplits = 8;
 constexpr int kMinKbPerSplit = 16;  // 1024 input channels per split at least
@@ -627,6 +714,8 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
   ka.M = pr.M;
   ka.K = pr.K;
   ka.kblocks = (int)ceil_div(pr.K, 64);
+  ka.wtiles = pr.wf ? (int)ceil_div(pr.K, kTileK4) : ka.kblocks;
+  ka.gshift = pr.gshift;
   ka.nproj = pr.nproj;
   auto fill = [&](const GemmPlan& q) {
     ka.tiles_m = q.tiles_m;
@@ -665,6 +754,7 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
   // strip (row stride ldx); fall back to 64-bit addressing when those could
   // overflow.
   if (p.cfg != kDmaM128N128 && !v3_offsets_fit(ka, p.bm, p.bn)) {
+    if (pr.wf != kWfInt8) return hipErrorInvalidValue;  // int4 tiles are half the span: not reached
     p.cfg = kDmaM128N128;
     set_tiles(p, pr.M, ns, pr.nproj);
     p.splits = 1;
@@ -674,6 +764,8 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
   if (p.splits > 1 && (!workspace || (int64_t)p.tiles_m * p.tiles_n > kMaxSplitTiles ||
                        gemm_workspace_bytes(p) >= (1ull << 31)))
     return hipErrorInvalidValue;
+  if (pr.wf == kWfInt4) return launch_gemm4<kWfInt4>(p.cfg, ka, stream);
+  if (pr.wf == kWfInt4Grp) return launch_gemm4<kWfInt4Grp>(p.cfg, ka, stream);
   switch (p.cfg) {
     case kV3M128N256: return launch_v3_t<128, 256, 1, 4, 2, 2>(ka, stream);
     case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3>(ka, stream);

@@ -71,6 +71,9 @@ struct GemvKernelArgs {
   // Fused argmax (nullptr: none): every workgroup's best key per row,
   // [M][gridDim.x], reduced by argmax_finish_kernel after this launch.
   unsigned long long* amax_slots;
+  // Group-wise int4: log2(group_size / 32); scale row of tile position k is
+  // k / group_size.
+  int gshift;
 };
 
 // Argmax key of output value v at column n: the fp16 value mapped to an
@@ -133,6 +136,26 @@ __device__ __forceinline__ void load_x_global(const GemvKernelArgs& a, int kb, c
   }
 }
 
+// Activation fragment of one int4 tile (128 input positions): lane l reads
+// x[m][128*kb + 32*(l/16) .. +31] as four half8, m = 16*mt + l%16, with the
+// same wave-uniform base plus fixed per-lane offset as above.  K % 64 == 0
+// for int4, so with KT (K % 128 == 64) a lane's 32 positions are either all
+// below K or all past it; the latter read a clamped chunk and are zeroed.
+template <int MT, bool KT>
+__device__ __forceinline__ void load_x_global4(const GemvKernelArgs& a, int kb, const uint32_t (&xoff)[MT],
+                                               int lane, half8 (&xa)[MT][4]) {
+  const uint8_t* xb = reinterpret_cast<const uint8_t*>(a.x) + (int64_t)kb * (kTileK4 * 2);
+  const int k = kb * kTileK4 + 32 * (lane >> 4);
+  const int d = KT ? (min(k, a.K - 32) - k) * 2 : 0;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const half8 v = as_half8(load_u4(xb + xoff[mt] + d + 16 * c));
+      xa[mt][c] = (!KT || k < a.K) ? v : half8{};
+    }
+}
+
 // The same fragment read from the LDS copy of x (row pitch `pitch` bytes,
 // column 0 = first K position of the split; the copy is zero past K).  Rows
 // m >= M read row M-1; tiles past the split read tile kl_max and are zeroed.
@@ -152,11 +175,32 @@ __device__ __forceinline__ void load_x_lds(const uint8_t* xs, int pitch, int M, 
   }
 }
 
-// Dynamic LDS bytes the kernel needs: max(x copy, cross-wave reduction).
-inline size_t gemv_lds_bytes(int MT, int NS, int W, bool XL, int M, int kb_per_split) {
+// The int4 fragment (four half8, positions 32*(l/16) .. +31 of the tile)
+// from the LDS copy of x; same conventions as load_x_lds.
+template <int MT>
+__device__ __forceinline__ void load_x_lds4(const uint8_t* xs, int pitch, int M, int kl, int kl_max,
+                                            int lane, half8 (&xa)[MT][4]) {
+  const bool valid = kl <= kl_max;
+  const int k = min(kl, kl_max) * kTileK4 + 32 * (lane >> 4);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = min(mt * 16 + (lane & 15), M - 1);
+    const uint8_t* p = xs + m * pitch + k * 2;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const half8 v = as_half8(*reinterpret_cast<const uint4*>(p + 16 * c));
+      xa[mt][c] = valid ? v : half8{};
+    }
+  }
+}
+
+// Dynamic LDS bytes the kernel needs: max(x copy, cross-wave reduction);
+// tk = input positions per weight tile (64 int8, 128 int4).
+inline size_t gemv_lds_bytes(int MT, int NS, int W, bool XL, int M, int kb_per_split,
+                             int tk = kTileK) {
   const size_t red = (size_t)W * MT * NS * kWave * sizeof(floatx4);
   // x copy, rounded up to whole 1 KB DMA chunks
-  const size_t xb = XL ? ((size_t)M * (size_t)(kb_per_split * kTileK * 2 + 16) + 1023) / 1024 * 1024 : 0;
+  const size_t xb = XL ? ((size_t)M * (size_t)(kb_per_split * tk * 2 + 16) + 1023) / 1024 * 1024 : 0;
   return red > xb ? red : xb;
 }
 
@@ -164,7 +208,7 @@ inline size_t gemv_lds_bytes(int MT, int NS, int W, bool XL, int M, int kb_per_s
 // at the group's counter sums every split in split order (deterministic),
 // applies scale and bias, stores fp16 (and feeds the fused argmax), and
 // re-zeroes the counter.  Returns whether this workgroup was the last.
-template <int NS>
+template <int NS, bool SC>
 __device__ __forceinline__ bool split_k_reduce(const GemvKernelArgs& a, int group, int strip0,
                                                int P_nstrips, int P_N, int P_col0,
                                                const _Float16* P_scale, const _Float16* P_bias,
@@ -199,7 +243,7 @@ __device__ __forceinline__ bool split_k_reduce(const GemvKernelArgs& a, int grou
     for (int sp = 1; sp < kMaxSplits; ++sp)
       if (sp < a.splits) sum += part[sp];
     if (n < P_N) {
-      const float sc = (float)P_scale[n];
+      const float sc = SC ? (float)P_scale[n] : 1.f;
       const float bi = P_bias ? (float)P_bias[n] : 0.f;
       const _Float16 v = (_Float16)__builtin_fmaf(sum, sc, bi);
       if (P_y) P_y[(int64_t)m * P_ldy + n] = v;
@@ -224,11 +268,18 @@ __device__ __forceinline__ void argmax_store(const GemvKernelArgs& a, const unsi
     a.amax_slots[(int64_t)m * gridDim.x + blockIdx.x] = row_key[m];
 }
 
-template <int MT, int NS, int W, int U, bool XL, bool NT, bool KT>
+// WF (WeightFormat): int8 tiles (64 input positions, two MFMAs per tile and
+// strip) or int4 tiles (128 positions, four MFMAs); group-wise int4 loads one
+// scale per lane, tile and strip alongside the weights and applies it at
+// dequantization, the other formats scale in the epilogue.
+template <int MT, int NS, int W, int U, bool XL, bool NT, bool KT, int WF = kWfInt8>
 __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int kThreads = W * kWave;
   constexpr int T = MT * NS;  // 16x16 output tiles per workgroup
+  constexpr int XN = WF ? 4 : 2;  // half8 activation chunks per tile and m-tile
+  constexpr int TK = WF ? kTileK4 : kTileK;  // input positions per weight tile
+  constexpr bool GS = WF == kWfInt4Grp;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
@@ -254,7 +305,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
 
   // LDS row pitch of the x copy: 128 B per tile (+16 B in the register-
   // staged K-tail path, so rows start on different banks).
-  const int pitch = XL ? ntiles * kTileK * 2 + (KT ? 16 : 0) : 0;
+  const int pitch = XL ? ntiles * TK * 2 + (KT ? 16 : 0) : 0;
 
   // CH independent accumulator chains (the two K halves of a tile, and
   // alternate tiles when registers allow): a single chain would make every
@@ -283,7 +334,18 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   uint32_t xoff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
-    xoff[mt] = (uint32_t)(min(mt * 16 + (lane & 15), a.M - 1) * a.ldx * 2) + 32 * (lane >> 4);
+    xoff[mt] = (uint32_t)(min(mt * 16 + (lane & 15), a.M - 1) * a.ldx * 2) + (WF ? 64 : 32) * (lane >> 4);
+  // Group-wise int4 scale of lane l, strip s, tile kl: scale row
+  // (4*(kb0 + kl) + l/16) >> gshift (4 lane groups of 32 positions per
+  // tile), column 16*strip + l%16.  Wave-uniform row part per tile, fixed
+  // per-lane part.
+  const _Float16* sstrip[GS ? NS : 1];
+  uint32_t slane = 0;
+  if (GS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) sstrip[s] = P_scale + 16 * min(strip0 + s, P_nstrips - 1);
+    slane = (uint32_t)(((lane >> 4) >> a.gshift) * P_N + (lane & 15));
+  }
 
   // Tiles of this wavefront: local index kl = wave + W*i, i in [0, my).
   // Every load below is unconditional: a tile past the split (the last
@@ -294,9 +356,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   const int stages = (my + U - 1) / U;
 
   uint4 wA[U][NS], wB[U][NS];
-  half8 xA[XL ? 1 : U][MT][2], xB[XL ? 1 : U][MT][2];
+  half8 xA[XL ? 1 : U][MT][XN], xB[XL ? 1 : U][MT][XN];
+  _Float16 sA[GS ? U : 1][NS], sB[GS ? U : 1][NS];
 
-  auto load_stage = [&](int st, uint4 (&wv)[U][NS], half8 (&xv)[XL ? 1 : U][MT][2]) {
+  auto load_stage = [&](int st, uint4 (&wv)[U][NS], half8 (&xv)[XL ? 1 : U][MT][XN],
+                        _Float16 (&sv)[GS ? U : 1][NS]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kl = wave + W * (st * U + u);
@@ -306,28 +370,68 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
         const uint8_t* p = wstrip[s] + (int64_t)klc * kTileBytes + woff;
         wv[u][s] = NT ? load_u4_stream(p) : load_u4(p);
       }
-      if (!XL) load_x_global<MT, KT>(a, kb0 + klc, xoff, lane, xv[XL ? 0 : u]);
+      if (GS) {
+        if (KT) {
+          // K % 128 == 64: the last tile's lanes 32..63 lie past K (their
+          // activations are zero); clamp their scale row into the matrix.
+          const int srow = min((4 * (kb0 + klc) + (lane >> 4)) >> a.gshift,
+                               (a.K >> (5 + a.gshift)) - 1);
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+            sv[GS ? u : 0][s] = sstrip[GS ? s : 0][(int64_t)srow * P_N + (lane & 15)];
+        } else {
+          const int srow = (4 * (kb0 + klc)) >> a.gshift;  // wave-uniform
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+            sv[GS ? u : 0][s] = sstrip[GS ? s : 0][(int64_t)srow * P_N + slane];
+        }
+      }
+      if constexpr (WF != kWfInt8) {
+        if (!XL) load_x_global4<MT, KT>(a, kb0 + klc, xoff, lane, xv[XL ? 0 : u]);
+      } else if (!XL) {
+        load_x_global<MT, KT>(a, kb0 + klc, xoff, lane, xv[XL ? 0 : u]);
+      }
     }
   };
 
-  auto compute_stage = [&](int st, const uint4 (&wv)[U][NS], half8 (&xv)[XL ? 1 : U][MT][2]) {
+  auto compute_stage = [&](int st, const uint4 (&wv)[U][NS], half8 (&xv)[XL ? 1 : U][MT][XN],
+                           const _Float16 (&sv)[GS ? U : 1][NS]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kl = wave + W * (st * U + u);
       if (kl >= ntiles) break;  // wave-uniform
-      half8 xl[MT][2];
-      if (XL) load_x_lds<MT>(smem, pitch, a.M, kl, ntiles - 1, lane, xl);
+      if constexpr (WF != kWfInt8) {
+        // Four MFMAs per tile and strip: dword j holds positions 8j..8j+7 of
+        // the lane's 32, matching activation chunk j.
+        half8 xl4[MT][4];
+        if (XL) load_x_lds4<MT>(smem, pitch, a.M, kl, ntiles - 1, lane, xl4);
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const half8 b0 = dequant8(wv[u][s].x, wv[u][s].y);
-        const half8 b1 = dequant8(wv[u][s].z, wv[u][s].w);
+        for (int s = 0; s < NS; ++s) {
+          const uint32_t wd[4] = {wv[u][s].x, wv[u][s].y, wv[u][s].z, wv[u][s].w};
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const half8 x0 = XL ? xl[mt][0] : xv[XL ? 0 : u][mt][0];
-          const half8 x1 = XL ? xl[mt][1] : xv[XL ? 0 : u][mt][1];
-          const int c = (2 * u) % CH;  // chains c (first K half), c+1 (second)
-          accs[c][mt][s] = mfma16x16x32(x0, b0, accs[c][mt][s]);
-          accs[c + 1][mt][s] = mfma16x16x32(x1, b1, accs[c + 1][mt][s]);
+          for (int j = 0; j < 4; ++j) {
+            const half8 b = GS ? dequant8_i4_scaled(wd[j], sv[GS ? u : 0][s]) : dequant8_i4(wd[j]);
+            const int c = (4 * u + j) % CH;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              accs[c][mt][s] = mfma16x16x32(XL ? xl4[mt][j] : xv[XL ? 0 : u][mt][j], b, accs[c][mt][s]);
+          }
+        }
+      } else {
+        half8 xl[MT][2];
+        if (XL) load_x_lds<MT>(smem, pitch, a.M, kl, ntiles - 1, lane, xl);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const half8 b0 = dequant8(wv[u][s].x, wv[u][s].y);
+          const half8 b1 = dequant8(wv[u][s].z, wv[u][s].w);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const half8 x0 = XL ? xl[mt][0] : xv[XL ? 0 : u][mt][0];
+            const half8 x1 = XL ? xl[mt][1] : xv[XL ? 0 : u][mt][1];
+            const int c = (2 * u) % CH;  // chains c (first K half), c+1 (second)
+            accs[c][mt][s] = mfma16x16x32(x0, b0, accs[c][mt][s]);
+            accs[c + 1][mt][s] = mfma16x16x32(x1, b1, accs[c + 1][mt][s]);
+          }
         }
       }
     }
@@ -343,24 +447,26 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)smem;
     for (int j = wave; j * 1024 < total; j += W) {
       const int pb = min(j * 1024 + lane * 16, total - 16);
-      const int m = pb / pitch, c = pb - m * pitch;
-      const uint8_t* src = reinterpret_cast<const uint8_t*>(a.x + (int64_t)m * a.ldx + kb0 * kTileK) + c;
+      int m = 0;  // pb / pitch, by M - 1 compares (x is staged for small M only)
+      for (int r = 1; r < a.M; ++r) m += pb >= r * pitch ? 1 : 0;
+      const int c = pb - m * pitch;
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(a.x + (int64_t)m * a.ldx + kb0 * TK) + c;
       dma16(src, lds0 + j * 1024);
     }
   }
   // The first two stages of weight tiles go out before anything waits.
-  if (stages > 0) load_stage(0, wA, xA);
-  if (stages > 1) load_stage(1, wB, xB);
+  if (stages > 0) load_stage(0, wA, xA, sA);
+  if (stages > 1) load_stage(1, wB, xB, sB);
 
   // ---- stage x[0:M, split's K range] in LDS (zero past K) ----------------
   if (XL && KT) {
     // Columns past K need zeros: staged through registers (after the first
     // weight tiles went out, so the two round trips overlap).
-    const int row_chunks = ntiles * (kTileK / 8);
+    const int row_chunks = ntiles * (TK / 8);
     const int total = a.M * row_chunks;
     for (int c = tid; c < total; c += kThreads) {
       const int m = c / row_chunks, cc = c - m * row_chunks;
-      const int k = kb0 * kTileK + cc * 8;
+      const int k = kb0 * TK + cc * 8;
       const uint4 v = load_u4(a.x + (int64_t)m * a.ldx + min(k, a.K - 8));
       *reinterpret_cast<uint4*>(smem + m * pitch + cc * 16) = k < a.K ? v : make_uint4(0, 0, 0, 0);
     }
@@ -369,8 +475,10 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
     // The DMAs were issued before the weight loads (xdma above): wait for
     // this wave's share (every load issued after them may stay in flight),
     // then for everyone's.
-    if (stages > 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * U * NS) : "memory");
-    else if (stages > 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(U * NS) : "memory");
+    // (loads per stage: U*NS weight tiles, and as many group scales)
+    constexpr int LPS = U * NS * (GS ? 2 : 1);
+    if (stages > 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPS) : "memory");
+    else if (stages > 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LPS) : "memory");
     else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     barrier_lds();
   }
@@ -378,11 +486,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   // Two-stage pipeline, unrolled by two so the buffers never move: a
   // stage's buffer is refilled (two stages ahead) as soon as it is consumed.
   for (int st = 0; st < stages; st += 2) {
-    compute_stage(st, wA, xA);
-    if (st + 2 < stages) load_stage(st + 2, wA, xA);
+    compute_stage(st, wA, xA, sA);
+    if (st + 2 < stages) load_stage(st + 2, wA, xA, sA);
     if (st + 1 >= stages) break;
-    compute_stage(st + 1, wB, xB);
-    if (st + 3 < stages) load_stage(st + 3, wB, xB);
+    compute_stage(st + 1, wB, xB, sB);
+    if (st + 3 < stages) load_stage(st + 3, wB, xB, sB);
   }
 
   floatx4 acc[MT][NS];
@@ -422,7 +530,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
     if (m >= a.M || strip0 + s >= P_nstrips) continue;
     if (a.splits == 1) {
       if (n < P_N) {
-        const float sc = (float)P_scale[n];
+        const float sc = GS ? 1.f : (float)P_scale[n];
         const float bi = P_bias ? (float)P_bias[n] : 0.f;
         const _Float16 v = (_Float16)__builtin_fmaf(sum, sc, bi);
         if (P_y) P_y[(int64_t)m * P_ldy + n] = v;
@@ -434,7 +542,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
       store_coherent(&a.partial[((int64_t)split * a.M + m) * a.np + P_col0 + n], sum);
     }
   }
-  if (a.splits > 1 && !split_k_reduce<NS>(a, group, strip0, P_nstrips, P_N, P_col0, P_scale,
+  if (a.splits > 1 && !split_k_reduce<NS, !GS>(a, group, strip0, P_nstrips, P_N, P_col0, P_scale,
                                           P_bias, P_y, P_ldy, amax, row_key, tid, kThreads))
     return;
   if (amax) argmax_store(a, row_key, tid, kThreads);
@@ -483,17 +591,17 @@ __global__ __launch_bounds__(kFinishThreads) void argmax_finish_kernel(
   if (tid == 0) index[m] = argmax_index_of(best[0]);
 }
 
-template <int MT, int NS, int W, int U, bool XL, bool NT>
+template <int MT, int NS, int W, int U, bool XL, bool NT, int WF = kWfInt8>
 hipError_t launch_t(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t stream) {
-  const size_t lds = gemv_lds_bytes(MT, NS, W, XL, ka.M, ka.kb_per_split);
+  const size_t lds = gemv_lds_bytes(MT, NS, W, XL, ka.M, ka.kb_per_split, WF ? kTileK4 : kTileK);
   if (lds > 65536) return hipErrorInvalidValue;
   dim3 grid(p.groups, p.splits, 1);
-  if ((ka.K % kTileK) != 0)  // K-tail variant: chunks past K are zeroed
-    hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, W, U, XL, NT, true>), grid, dim3(W * kWave), lds,
-                       stream, ka);
+  if ((ka.K % (WF ? kTileK4 : kTileK)) != 0)  // K-tail variant: chunks past K are zeroed
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, W, U, XL, NT, true, WF>), grid, dim3(W * kWave),
+                       lds, stream, ka);
   else
-    hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, W, U, XL, NT, false>), grid, dim3(W * kWave), lds,
-                       stream, ka);
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MT, NS, W, U, XL, NT, false, WF>), grid, dim3(W * kWave),
+                       lds, stream, ka);
   return hipGetLastError();
 }
 
@@ -503,7 +611,9 @@ GemvKernelArgs make_args(const LinearProblem& pr, const GemvPlan& p, void* works
   ka.ldx = pr.ldx;
   ka.M = pr.M;
   ka.K = pr.K;
-  ka.kblocks = (int)ceil_div(pr.K, 64);
+  // Weight tiles along K: 64 input positions per int8 tile, 128 per int4 tile.
+  ka.kblocks = (int)ceil_div(pr.K, pr.wf ? kTileK4 : kTileK);
+  ka.gshift = pr.gshift;
   ka.nproj = pr.nproj;
   int group = 0, col = 0;
   for (int i = 0; i < kMaxProj; ++i) {
@@ -593,6 +703,40 @@ hipError_t launch_gemv_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStrea
   }
 }
 
+// Int4 launches take the same rules with K counted in 128-wide tiles (one
+// 1 KB tile per 128 positions, as an int8 tile holds 64): a configuration
+// runs with half its unroll (its int4 tiles carry twice the activation
+// registers), and activations always come from global memory.
+template <int WF>
+hipError_t launch_gemv4_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t stream) {
+  // x staged in LDS where the planner asks for it and int4's 256 bytes of x
+  // per row and tile still fit.
+  auto xl_fits = [&](int ns, int w) {
+    return gemv_lds_bytes(1, ns, w, true, ka.M, ka.kb_per_split, kTileK4) <= 65536;
+  };
+  switch (p.cfg) {
+    case kG1x1W16U4XL:
+      if (xl_fits(1, 16)) return launch_t<1, 1, 16, 1, true, true, WF>(ka, p, stream);
+      return launch_t<1, 1, 16, 1, false, true, WF>(ka, p, stream);
+    case kG1x1W8U4XL:
+      if (xl_fits(1, 8)) return launch_t<1, 1, 8, 2, true, true, WF>(ka, p, stream);
+      return launch_t<1, 1, 8, 2, false, true, WF>(ka, p, stream);
+    case kG1x1W16U2: return launch_t<1, 1, 16, 1, false, true, WF>(ka, p, stream);
+    case kG1x1W8U4: return launch_t<1, 1, 8, 2, false, true, WF>(ka, p, stream);
+    case kG1x1W4U4: return launch_t<1, 1, 4, 2, false, true, WF>(ka, p, stream);
+    case kG1x2W16U2: return launch_t<1, 2, 16, 1, false, true, WF>(ka, p, stream);
+    case kG1x4W8U2: return launch_t<1, 4, 8, 1, false, true, WF>(ka, p, stream);
+    case kG1x4W4U2: return launch_t<1, 4, 4, 1, false, true, WF>(ka, p, stream);
+    case kG1x2W8U2: return launch_t<1, 2, 8, 1, false, true, WF>(ka, p, stream);
+    case kG2x4W4U2: return launch_t<2, 4, 4, 1, false, true, WF>(ka, p, stream);
+    case kG2x2W8U1: return launch_t<2, 2, 8, 1, false, true, WF>(ka, p, stream);
+    case kG2x1W8U4: return launch_t<2, 1, 8, 2, false, true, WF>(ka, p, stream);
+    case kG4x2W8U1: return launch_t<4, 2, 8, 1, false, true, WF>(ka, p, stream);
+    case kG4x2W4U1: return launch_t<4, 2, 4, 1, false, true, WF>(ka, p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
 
 size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj) {
@@ -606,6 +750,11 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
                        hipStream_t stream, const ArgmaxTarget* am) {
   if (pr.nproj < 1 || pr.nproj > kMaxProj) return hipErrorInvalidValue;
   GemvKernelArgs ka = make_args(pr, p, workspace);
+  if (pr.wf != kWfInt8) {
+    if (am) return hipErrorInvalidValue;
+    return pr.wf == kWfInt4 ? launch_gemv4_cfg<kWfInt4>(ka, p, stream)
+                            : launch_gemv4_cfg<kWfInt4Grp>(ka, p, stream);
+  }
   if (am) {
     if (pr.nproj != 1 || pr.M > 64 || !am->slots || !am->index) return hipErrorInvalidValue;
     ka.amax_slots = reinterpret_cast<unsigned long long*>(am->slots);
@@ -619,6 +768,40 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
 }
 
 size_t argmax_slot_bytes(const GemvPlan& p, int M) { return (size_t)M * (size_t)p.groups * 8; }
+
+// Int4 launches: the int8 rules over K counted in 128-wide tiles (one 1 KB
+// tile per 128 positions), with two changes measured on the cfg1 shapes
+// (MI355X): at M 3..4 with many strips the activations are staged in LDS
+// (an int4 tile reads four activation chunks per weight load, so the LDS
+// copy pays off beyond M = 2), and at M 5..16 a long K with few strips
+// takes two strips per workgroup and a 2-way K split.
+GemvPlan plan_gemv_int4(int M, int N, int K, const DeviceInfo& dev) {
+  const int keff = (int)(round_up(K, kTileK4) / 2);
+  GemvPlan p = plan_gemv(M, &N, 1, keff, dev);
+  const int ktiles = (int)ceil_div(K, kTileK4);
+  const int nstrips = (int)ceil_div(N, 16);
+  const int cu = dev.cus > 0 ? dev.cus : 256;
+  auto fits_xl = [&](int w) { return gemv_lds_bytes(1, 1, w, true, M, ktiles, kTileK4) <= 65536; };
+  int cfg = p.cfg, splits = p.splits;
+  if (M >= 3 && M <= 4 && cfg == kG1x2W8U2 && fits_xl(8)) {
+    cfg = kG1x1W8U4XL;
+  } else if (M >= 5 && M <= 16 && cfg == kG1x1W16U2 && ktiles >= 64 &&
+             (int64_t)nstrips * 256 <= 511LL * cu) {
+    cfg = kG1x2W8U2;
+    splits = 2;
+  }
+  if (cfg == p.cfg) return p;
+  GemvPlan q;
+  q.cfg = cfg;
+  q.mt = kGemvCfgs[cfg].mt;
+  q.ns = kGemvCfgs[cfg].ns;
+  q.groups = (int)ceil_div(nstrips, q.ns);
+  if (q.groups > kMaxGroupsSplit) splits = 1;
+  if (splits > ktiles) splits = ktiles;
+  q.kb_per_split = (int)ceil_div(ktiles, splits);
+  q.splits = (int)ceil_div(ktiles, q.kb_per_split);
+  return q;
+}
 
 
 // Kernel choice per shape: the analogue of the reference's W8A16 tile

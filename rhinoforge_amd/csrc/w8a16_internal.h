@@ -16,8 +16,8 @@ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 // output) and a launch of up to RF_W8A16_MAX_PROJ projections sharing x,
 // already validated.
 struct Projection {
-  const uint8_t* w;      // TILE16X64 packed
-  const _Float16* scale; // [N]
+  const uint8_t* w;      // TILE16X64 (int8) or TILE16X128_I4 (int4) packed
+  const _Float16* scale; // [N], or [K/group][N] for group-wise int4
   const _Float16* bias;  // [N] or nullptr
   _Float16* y;
   int64_t ldy;
@@ -30,6 +30,8 @@ struct LinearProblem {
   int M, K;
   int nproj;
   Projection proj[RF_W8A16_MAX_PROJ];
+  int wf = 0;      // weight format (w8a16_common.h WeightFormat): 0 int8, 1 int4, 2 int4 group-wise
+  int gshift = 0;  // group-wise int4: log2(group_size / 32)
 };
 
 // Decode GEMV / skinny-GEMM launch plan (M <= 64).
@@ -62,6 +64,8 @@ int device_info(DeviceInfo* out);
 
 GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev);
 GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev);
+// GEMV plan of a packed-int4 weight (one projection).
+GemvPlan plan_gemv_int4(int M, int N, int K, const DeviceInfo& dev);
 // Workspace bytes past the RF_W8A16_WS_COUNTER_BYTES counter region.
 size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj);
 size_t gemm_workspace_bytes(const GemmPlan& p);
@@ -84,6 +88,8 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
                        hipStream_t stream, const ArgmaxTarget* am = nullptr);
 hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& p, void* workspace,
                        hipStream_t stream);
+hipError_t launch_pack4(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* dst,
+                        hipStream_t stream);
 hipError_t launch_pack(const int8_t* q, int64_t N, int64_t K, int64_t ldq,
                        uint8_t* dst, hipStream_t stream);
 

@@ -10,6 +10,11 @@
 //   pack_weight(Tensor q) -> Tensor
 //   unpack_weight(Tensor packed, int N, int K) -> Tensor
 //   select_kernel(int M, int N, int K) -> int
+// and (namespace `w4a16`, packed int4 weights, rf_w4a16_* in the C ABI):
+//   linear(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias=None,
+//          int kernel=0) -> Tensor
+//   pack_weight(Tensor q) -> Tensor
+//   unpack_weight(Tensor packed, int N, int K) -> Tensor
 //
 // These mirror the reference's eager FP16 `linear_into` (schema at
 // src/core/rpu_dispatch_registrations.inc:19-20, checks at
@@ -339,6 +344,139 @@ at::Tensor unpack_weight(const at::Tensor& packed, int64_t N, int64_t K) {
   return q;
 }
 
+// ---- W4A16 -------------------------------------------------------------------
+// The reference's launcher takes a packed-int4 weight as a uint8 [N, K/2]
+// tensor and tells per-channel from group-wise by the scale's rank
+// (src/ops/rpu_linear.cpp:1211-1489); so does this op: weight uint8
+// TILE16X128_I4 [ceil16(N), ceil128(K)/2], scale fp16 [N] (per-channel) or
+// [G, N] (group-wise, group_size = K / G in {32, 64, 128}).
+at::Tensor w4_linear_hip(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                         const c10::optional<at::Tensor>& bias, int64_t kernel) {
+  RECORD_FUNCTION("w4a16::linear", {});
+  const char* op = "w4a16::linear";
+  TORCH_CHECK(input.scalar_type() == at::kHalf, op, ": input must be float16, got ",
+              input.scalar_type());
+  TORCH_CHECK(weight.scalar_type() == at::kByte, op,
+              ": weight must be uint8 (packed int4, use w4a16.pack_weight), got ",
+              weight.scalar_type());
+  TORCH_CHECK(scale.scalar_type() == at::kHalf, op, ": weight_scale must be float16, got ",
+              scale.scalar_type());
+  TORCH_CHECK(input.dim() >= 1, op, ": input must have at least one dimension");
+  TORCH_CHECK(input.is_cuda() && weight.is_cuda() && scale.is_cuda(), op,
+              ": input, weight and weight_scale must be on a HIP device (there is no CPU "
+              "implementation)");
+  TORCH_CHECK(input.device() == weight.device() && input.device() == scale.device(), op,
+              ": input, weight and weight_scale must be on the same device");
+  TORCH_CHECK((scale.dim() == 1 || scale.dim() == 2) && scale.is_contiguous(), op,
+              ": weight_scale must be a contiguous [N] (per-channel) or [K/group_size, N] "
+              "(group-wise) tensor, got ", scale.sizes());
+  const int64_t K = input.size(-1);
+  const int64_t N = scale.size(-1);
+  int64_t group_size = 0;
+  if (scale.dim() == 2) {
+    const int64_t G = scale.size(0);
+    TORCH_CHECK(G >= 1 && K % G == 0, op, ": group-wise scale has ", G,
+                " rows, which does not divide K=", K);
+    group_size = K / G;
+    TORCH_CHECK(group_size == 32 || group_size == 64 || group_size == 128, op,
+                ": group size K / scale.size(0) = ", group_size, " must be 32, 64 or 128");
+  }
+  TORCH_CHECK(N >= 16 && N % 16 == 0, op, ": out_features N=", N,
+              " must be a positive multiple of 16 for packed int4");
+  TORCH_CHECK(K >= 64 && K % 64 == 0, op, ": in_features K=", K,
+              " must be a positive multiple of 64 for packed int4");
+  TORCH_CHECK(weight.is_contiguous() && weight.dim() == 2 && weight.size(0) == N &&
+                  weight.size(1) == ceil_to(K, 128) / 2,
+              op, ": packed weight must be contiguous uint8 [", N, ", ", ceil_to(K, 128) / 2,
+              "] for N=", N, ", K=", K, " (use w4a16.pack_weight), got ", weight.sizes());
+  if (bias.has_value() && bias->defined()) {
+    const at::Tensor& b = *bias;
+    TORCH_CHECK(b.scalar_type() == at::kHalf, op, ": bias must be float16");
+    TORCH_CHECK(b.is_cuda() && b.device() == input.device(), op,
+                ": bias must be on the input's device");
+    TORCH_CHECK(b.dim() == 1 && b.size(0) == N && b.is_contiguous(), op,
+                ": bias must be a contiguous vector with ", N, " elements, got shape ", b.sizes());
+  }
+  const int64_t M = input.numel() / K;
+  std::vector<int64_t> shape = input.sizes().vec();
+  shape.back() = N;
+  at::Tensor y2 = at::empty({M, N}, input.options());
+  if (M == 0) return y2.view(shape);
+  at::Tensor x2 = input.reshape({M, K});
+  const bool ok = x2.stride(1) == 1 && x2.stride(0) % 8 == 0 &&
+                  (reinterpret_cast<uintptr_t>(x2.data_ptr()) % 16) == 0;
+  if (!ok) x2 = x2.is_contiguous() ? x2.clone() : x2.contiguous();
+  // group-wise scale rows are copied with 16-byte DMAs
+  at::Tensor sc = (group_size && reinterpret_cast<uintptr_t>(scale.data_ptr()) % 16) ? scale.clone()
+                                                                                      : scale;
+  c10::DeviceGuard dev_guard(x2.device());
+  void* stream = c10::hip::getCurrentHIPStream(x2.device().index()).stream();
+  const size_t ws_bytes = rf_w4a16_workspace_bytes(M, N, K);
+  TORCH_CHECK(ws_bytes > 0, op, ": ", rf_w8a16_status_str(RF_W8A16_EINVAL));
+  at::Tensor ws = workspace_cache().get(x2.device(), stream, ws_bytes);
+  const void* bptr = (bias.has_value() && bias->defined()) ? bias->data_ptr() : nullptr;
+  check_status(rf_w4a16_linear(x2.data_ptr(), x2.stride(0), weight.data_ptr(), sc.data_ptr(),
+                               (int32_t)group_size, bptr, y2.data_ptr(), N, M, N, K,
+                               (int32_t)kernel, ws.data_ptr(), (size_t)ws.numel(), stream),
+               op);
+  return y2.view(shape);
+}
+
+at::Tensor w4_linear_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                         const c10::optional<at::Tensor>&, int64_t) {
+  TORCH_CHECK(false, "w4a16::linear: tensors are on the CPU; the W4A16 kernels run on a HIP "
+              "device (gfx950) only and there is no CPU implementation");
+}
+
+at::Tensor w4_linear_meta(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                          const c10::optional<at::Tensor>& bias, int64_t kernel) {
+  std::vector<int64_t> shape = input.sizes().vec();
+  TORCH_CHECK(!shape.empty() && (scale.dim() == 1 || scale.dim() == 2), "w4a16::linear: bad shapes");
+  shape.back() = scale.size(-1);
+  return at::empty(shape, input.options());
+}
+
+// Int8 containers [N, K] holding int4 values in [-8, 7] -> TILE16X128_I4
+// (uint8).  CPU tensors are packed (and range-checked) on the host, HIP
+// tensors on the device.
+at::Tensor w4_pack_weight(const at::Tensor& q) {
+  TORCH_CHECK(q.scalar_type() == at::kChar, "w4a16::pack_weight: q must be int8 (int4 values), got ",
+              q.scalar_type());
+  TORCH_CHECK(q.dim() == 2, "w4a16::pack_weight: q must be 2-D [N, K], got ", q.sizes());
+  const int64_t N = q.size(0), K = q.size(1);
+  TORCH_CHECK(N >= 1 && K >= 1, "w4a16::pack_weight: empty weight ", q.sizes());
+  at::Tensor qc = q.contiguous();
+  at::Tensor out = at::empty({ceil_to(N, 16), ceil_to(K, 128) / 2}, q.options().dtype(at::kByte));
+  const size_t bytes = rf_w4a16_packed_bytes(N, K);
+  TORCH_CHECK((size_t)out.numel() == bytes, "w4a16::pack_weight: size mismatch");
+  if (q.is_cuda()) {
+    c10::DeviceGuard dev_guard(q.device());
+    void* stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
+    check_status(rf_w4a16_pack_weight_device(qc.data_ptr<int8_t>(), N, K, K, out.data_ptr(), bytes,
+                                             stream),
+                 "w4a16::pack_weight");
+  } else {
+    TORCH_CHECK(q.device().is_cpu(), "w4a16::pack_weight: unsupported device ", q.device());
+    const int st = rf_w4a16_pack_weight(qc.data_ptr<int8_t>(), N, K, K, out.data_ptr(), bytes);
+    TORCH_CHECK(st == RF_W8A16_OK, "w4a16::pack_weight: ", rf_w8a16_status_str(st),
+                " (int4 values must lie in [-8, 7])");
+  }
+  return out;
+}
+
+at::Tensor w4_unpack_weight(const at::Tensor& packed, int64_t N, int64_t K) {
+  TORCH_CHECK(packed.scalar_type() == at::kByte, "w4a16::unpack_weight: packed must be uint8");
+  TORCH_CHECK(N >= 1 && K >= 1, "w4a16::unpack_weight: N and K must be >= 1");
+  TORCH_CHECK(packed.numel() == (int64_t)rf_w4a16_packed_bytes(N, K),
+              "w4a16::unpack_weight: packed has ", packed.numel(), " bytes, expected ",
+              rf_w4a16_packed_bytes(N, K));
+  at::Tensor p = packed.to(at::kCPU).contiguous();
+  at::Tensor q = at::empty({N, K}, p.options().dtype(at::kChar));
+  check_status(rf_w4a16_unpack_weight(p.data_ptr(), N, K, q.data_ptr<int8_t>(), K),
+               "w4a16::unpack_weight");
+  return q;
+}
+
 int64_t select_kernel(int64_t M, int64_t N, int64_t K) {
   const int k = rf_w8a16_select_kernel(M, N, K);
   TORCH_CHECK(k > 0, "w8a16::select_kernel: ", rf_w8a16_status_str(-k));
@@ -377,3 +515,14 @@ TORCH_LIBRARY_IMPL(w8a16, CPU, m) {
   m.impl("linear_multi", TORCH_FN(linear_multi_cpu));
   m.impl("linear_argmax", TORCH_FN(linear_argmax_cpu));
 }
+
+TORCH_LIBRARY(w4a16, m) {
+  m.def("linear(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias=None, "
+        "int kernel=0) -> Tensor");
+  m.def("pack_weight(Tensor q) -> Tensor", TORCH_FN(w4_pack_weight));
+  m.def("unpack_weight(Tensor packed, int N, int K) -> Tensor", TORCH_FN(w4_unpack_weight));
+}
+
+TORCH_LIBRARY_IMPL(w4a16, CUDA, m) { m.impl("linear", TORCH_FN(w4_linear_hip)); }
+TORCH_LIBRARY_IMPL(w4a16, Meta, m) { m.impl("linear", TORCH_FN(w4_linear_meta)); }
+TORCH_LIBRARY_IMPL(w4a16, CPU, m) { m.impl("linear", TORCH_FN(w4_linear_cpu)); }

@@ -81,6 +81,96 @@ class W8A16Linear(nn.Module):
                 f"bias={self.bias is not None}, layout=TILE16X64")
 
 
+class W4A16Linear(nn.Module):
+    """Linear layer with packed int4 weights and fp16 scales (W4A16).
+
+    The reference replaces an fp16 ``nn.Linear``'s weight by a packed uint8
+    ``[N, K/2]`` Parameter and registers the scale as a ``weight_scale``
+    buffer: ``[N]`` per-channel, or the group-wise payload
+    (quant/convert_qwen3_w4a16.py:79-121).  Here ``weight`` is the
+    TILE16X128_I4 buffer, ``weight_scale`` is ``[N]`` or the logical
+    ``[K/group_size, N]``, and forward calls ``torch.ops.w4a16.linear``.
+    """
+
+    def __init__(self, in_features: int, out_features: int, group_size: int | None = 32,
+                 bias: bool = False, device=None) -> None:
+        super().__init__()
+        if in_features < 64 or in_features % 64:
+            raise ValueError(f"in_features={in_features} must be a positive multiple of 64")
+        if out_features < 16 or out_features % 16:
+            raise ValueError(f"out_features={out_features} must be a positive multiple of 16")
+        if group_size not in (None, 32, 64, 128) or (group_size and in_features % group_size):
+            raise ValueError(f"group_size={group_size} must be None (per-channel) or 32/64/128 "
+                             f"dividing in_features={in_features}")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.group_size = group_size
+        self.layout = ops.LAYOUT_TILE16X128_I4
+        self.register_buffer("weight", torch.full(ops.packed_shape_int4(out_features, in_features),
+                                                  0x88, dtype=torch.uint8, device=device))
+        sshape = (in_features // group_size, out_features) if group_size else (out_features,)
+        self.register_buffer("weight_scale", torch.ones(sshape, dtype=torch.float16, device=device))
+        if bias:
+            self.register_buffer("bias", torch.zeros(out_features, dtype=torch.float16,
+                                                     device=device))
+        else:
+            self.bias = None
+
+    @classmethod
+    def from_quantized(cls, q: torch.Tensor, weight_scale: torch.Tensor,
+                       bias: torch.Tensor | None = None, *, device=None) -> "W4A16Linear":
+        """From int4 values in int8 containers [N, K] and a scale [N] or
+        [K/group_size, N] (quant/int4_pack.py:21-23, int4_pgrp_pack.py:33-60)."""
+        if q.dtype != torch.int8 or q.dim() != 2:
+            raise TypeError(f"q must be int8 [N, K] int4 values, got {q.dtype} {tuple(q.shape)}")
+        n, k = q.shape
+        if weight_scale.dtype != torch.float16 or weight_scale.dim() not in (1, 2):
+            raise TypeError(f"weight_scale must be fp16 [N] or [G, N], got {weight_scale.dtype} "
+                            f"{tuple(weight_scale.shape)}")
+        if weight_scale.dim() == 1:
+            group_size = None
+            if tuple(weight_scale.shape) != (n,):
+                raise ValueError(f"per-channel scale must be [{n}], got {tuple(weight_scale.shape)}")
+        else:
+            g = weight_scale.shape[0]
+            if weight_scale.shape[1] != n or g < 1 or k % g:
+                raise ValueError(f"group-wise scale must be [K/group_size, {n}], got "
+                                 f"{tuple(weight_scale.shape)}")
+            group_size = k // g
+        device = torch.device(device) if device is not None else q.device
+        mod = cls(k, n, group_size=group_size, bias=bias is not None, device="meta")
+        mod.weight = ops.pack_weight_int4(q.to(device))
+        mod.weight_scale = weight_scale.to(device).contiguous()
+        if bias is not None:
+            mod.bias = bias.to(device=device, dtype=torch.float16).contiguous()
+        return mod
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, group_size: int | None = 32) -> "W4A16Linear":
+        """Quantize a floating nn.Linear (group-wise by default, as the
+        reference's W4A16 converter, convert_qwen3_w4a16.py:40-42), then pack."""
+        from .quant.int4 import quantize_int4_group_wise, quantize_int4_per_channel
+        w = linear.weight.detach()
+        if group_size:
+            q, s, _ = quantize_int4_group_wise(w, group_size)
+        else:
+            q, s = quantize_int4_per_channel(w)
+        b = linear.bias.detach().to(torch.float16) if linear.bias is not None else None
+        return cls.from_quantized(q, s, b)
+
+    def rowmajor_weight(self) -> torch.Tensor:
+        """The int4 values as an int8 [N, K] tensor (CPU)."""
+        return ops.unpack_weight_int4(self.weight, self.out_features, self.in_features)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return ops.linear_w4a16(x, self.weight, self.weight_scale, self.bias)
+
+    def extra_repr(self) -> str:
+        mode = f"group_size={self.group_size}" if self.group_size else "per-channel"
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, {mode}, layout=TILE16X128_I4")
+
+
 class W8A16Embedding(nn.Module):
     """Token embedding with an int8 row-major table and one fp16 scale per row.
 

@@ -61,9 +61,9 @@ def linear_multi(input: torch.Tensor, weights, weight_scales, biases=None, *,
     """Several projections of one input (q/k/v, gate/up) in one decode launch.
 
     Returns [input . (s_i (.) q_i)^T (+ b_i)] for each (weight_i, weight_scale_i,
-    bias_i).  With M <= 64 all projections run in a single GEMV launch (the
+    bias_i).  All projections run in one launch of either kernel (the
     analogue of the reference's fused QKV W8A16 kernel,
-    src/ops/rpu_linear.cpp:1546-1674); larger M runs one GEMM per projection.
+    src/ops/rpu_linear.cpp:1546-1674).
     """
     weights = list(weights)
     if biases is None:
@@ -93,3 +93,43 @@ def linear_argmax(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch
 def select_kernel(m: int, n: int, k: int) -> int:
     """Kernel the AUTO policy runs for (M, N, K): KERNEL_GEMV or KERNEL_GEMM."""
     return int(torch.ops.w8a16.select_kernel(m, n, k))
+
+
+# ---- W4A16 (packed int4 weights) ---------------------------------------------
+
+LAYOUT_TILE16X128_I4 = 2
+
+
+def packed_shape_int4(n: int, k: int) -> tuple[int, int]:
+    """Shape of the packed uint8 int4 weight for a logical [n, k] weight."""
+    return ((n + 15) // 16 * 16, (k + 127) // 128 * 64)
+
+
+def pack_weight_int4(q: torch.Tensor) -> torch.Tensor:
+    """int4 values in int8 containers [N, K] (range [-8, 7]) -> TILE16X128_I4
+    packed uint8 [ceil16(N), ceil128(K)/2].
+
+    Replaces the reference's nibble packers (quant/int4_pack.py:45-58,
+    quant/int4_pgrp_pack.py:158-162) with one layout for both scale modes.
+    Runs on the device for HIP tensors and on the host (range-checked) for
+    CPU tensors.
+    """
+    return torch.ops.w4a16.pack_weight(q)
+
+
+def unpack_weight_int4(packed: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """Inverse of :func:`pack_weight_int4`; returns a CPU int8 [n, k] tensor."""
+    return torch.ops.w4a16.unpack_weight(packed, n, k)
+
+
+def linear_w4a16(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                 bias: torch.Tensor | None = None, *, kernel: int = KERNEL_AUTO) -> torch.Tensor:
+    """y = input . W^T (+ bias) with a packed int4 weight, fp16 out, fp32 accumulation.
+
+    weight_scale fp16 [N] selects per-channel scaling (W = s[n] q[n,k], scale
+    applied to the fp32 sum); [K/group_size, N] selects group-wise scaling
+    (W = RN_fp16(s[k/gs, n] q[n,k]), group_size 32, 64 or 128), the dispatch
+    of the reference's launcher (src/ops/rpu_linear.cpp:1211-1489).  Needs
+    N % 16 == 0 and K % 64 == 0.  HIP tensors only.
+    """
+    return torch.ops.w4a16.linear(input, weight, weight_scale, bias, kernel)

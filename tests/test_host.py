@@ -23,7 +23,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def declared_functions() -> list[str]:
     text = (ROOT / "include" / "w8a16.h").read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(rf_w8a16_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(rf_w[48]a16_\w+)\s*\(", text)))
 
 
 def test_header_declares_expected_entry_points():
@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(capi.LIB_PATH))
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert capi.load().rf_w8a16_abi_version() == 1
+    assert capi.load().rf_w8a16_abi_version() == 2
 
 
 def test_status_strings():
