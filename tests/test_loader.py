@@ -320,3 +320,33 @@ def test_replicate_kv_heads_packed_matches_rowmajor(tmp_path, head_dim):
         load.replicate_kv_heads(fresh, 3)
     with pytest.raises(ValueError, match="divisible"):
         load.replicate_kv_heads(fresh, 8)
+
+
+def test_qwen3_vl_checkpoint_loads_with_text_projections_swapped(tmp_path):
+    """The VL family (AutoModelForImageTextToText): the text decoder's seven
+    projections per layer become W8A16Linear; the vision tower stays floating
+    (its attn.qkv / mlp.linear_fc* names are not quantized projections,
+    quant/convert_qwen3.py:25-33)."""
+    if not hasattr(transformers, "Qwen3VLConfig"):
+        pytest.skip("transformers without Qwen3-VL")
+    torch.manual_seed(0)
+    cfg = transformers.Qwen3VLConfig(
+        text_config=dict(vocab_size=512, hidden_size=128, intermediate_size=256,
+                         num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                         head_dim=32, max_position_embeddings=256,
+                         rope_scaling={"rope_type": "default", "mrope_section": [4, 6, 6]}),
+        vision_config=dict(depth=2, hidden_size=64, intermediate_size=128, num_heads=2,
+                           out_hidden_size=128, deepstack_visual_indexes=[1], patch_size=16,
+                           temporal_patch_size=2, spatial_merge_size=2))
+    transformers.Qwen3VLForConditionalGeneration(cfg).save_pretrained(
+        tmp_path / "src", safe_serialization=True)
+    stats = convert.convert_checkpoint(tmp_path / "src", tmp_path / "dst", log=lambda *a: None)
+    assert stats["n_quantized"] == 2 * 7
+    model = load.load_w8a16_model(None, tmp_path / "dst", device="cpu")
+    assert type(model).__name__ == "Qwen3VLForConditionalGeneration"
+    assert load.detect_and_validate_decoder_w8a16(model.model.language_model)
+    assert not any(isinstance(m, rf.W8A16Linear) for m in model.model.visual.modules())
+    ck = read_all(tmp_path / "dst")
+    for name, mod in model.named_modules():
+        if isinstance(mod, rf.W8A16Linear):
+            assert torch.equal(mod.rowmajor_weight(), ck[name + ".weight"]), name
