@@ -349,10 +349,10 @@ def bench_other_configs(torch, rf):
                                cs, 20 if m < 512 else 6)
             n = sum(QWEN3_VL_32B[i][1] for i in idxs)
             b = sum(nbytes(m, QWEN3_VL_32B[i][1], 5120) - 2 * m * 5120 for i in idxs) + 2 * m * 5120
+            kern = "gemv" if rf.select_kernel(m, n, 5120) == rf.KERNEL_GEMV else "gemm"
             r = {"M": m, "proj": name, "N": n, "K": 5120, "us": round(us, 2),
-                 "kernel": ("gemv" if m <= 64 else "gemm") + " (one launch)",
-                 "GBps": round(b / (us * 1e-6) / 1e9, 1)}
-            if m > 64:
+                 "kernel": kern + " (one launch)", "GBps": round(b / (us * 1e-6) / 1e9, 1)}
+            if kern == "gemm":
                 r["TFLOPs"] = round(2 * m * n * 5120 / (us * 1e-6) / 1e12, 1)
             rows.append(r)
     out["cfg4_vl32b"] = rows

@@ -66,7 +66,9 @@ typedef enum rf_w8a16_status {
 
 /* Kernel choice (the analogue of `force_gemm`, rpu_linear.cpp:1094-1103). */
 #define RF_W8A16_KERNEL_AUTO 0
-#define RF_W8A16_KERNEL_GEMV 1 /* decode GEMV / skinny GEMM, M <= 64       */
+#define RF_W8A16_KERNEL_GEMV 1 /* decode GEMV / skinny GEMM, M <= 64 (AUTO: M <= 16, M <= 28
+                                  with N*K <= 2^24, M <= 32 with N*K <= 2^23;
+                                  W4A16: M <= 64)                             */
 #define RF_W8A16_KERNEL_GEMM 2 /* LDS-staged dequant-into-MFMA GEMM         */
 
 /* Human-readable text for a status code; never NULL. */

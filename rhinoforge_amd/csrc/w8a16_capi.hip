@@ -142,8 +142,22 @@ int check_nk(int64_t N, int64_t K) {
   return RF_W8A16_OK;
 }
 
-// Kernel the AUTO policy picks; GEMV covers M <= 64, the GEMM everything.
-int auto_kernel(int64_t M) { return M <= 64 ? RF_W8A16_KERNEL_GEMV : RF_W8A16_KERNEL_GEMM; }
+// Kernel the AUTO policy picks (N summed over a launch's projections).
+// Measured on MI355X over the Qwen3-8B and Qwen3-VL-32B projections: the
+// GEMV wins up to M = 16; from M = 17 the small-tile split-K GEMM wins on
+// every shape but small weights, where the GEMV keeps a ~1 us lead (N*K <=
+// 2^24 up to M = 28, N*K <= 2^23 up to M = 32).  The GEMV runs up to M = 64
+// when forced.
+int auto_kernel(int64_t M, int64_t N, int64_t K) {
+  if (M <= 16) return RF_W8A16_KERNEL_GEMV;
+  const int64_t nk = N * K;
+  if ((M <= 28 && nk <= ((int64_t)1 << 24)) || (M <= 32 && nk <= ((int64_t)1 << 23)))
+    return RF_W8A16_KERNEL_GEMV;
+  return RF_W8A16_KERNEL_GEMM;
+}
+
+// W4A16 keeps the GEMV up to its M = 64 limit (its GEMM has no small tiles).
+int auto_kernel_int4(int64_t M) { return M <= 64 ? RF_W8A16_KERNEL_GEMV : RF_W8A16_KERNEL_GEMM; }
 
 }  // namespace
 
@@ -225,7 +239,7 @@ int rf_w8a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K, int64
 
 int rf_w8a16_select_kernel(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return -RF_W8A16_EINVAL;
-  return auto_kernel(M);
+  return auto_kernel(M, N, K);
 }
 
 size_t rf_w8a16_workspace_bytes_multi(int64_t M, const int64_t* Ns, int32_t count, int64_t K) {
@@ -278,7 +292,11 @@ int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w
   if (st != RF_W8A16_OK) return st;
   if (!dev.gfx950) return RF_W8A16_EDEVICE;
 
-  if (kernel == RF_W8A16_KERNEL_AUTO) kernel = auto_kernel(M);
+  if (kernel == RF_W8A16_KERNEL_AUTO) {
+    int64_t ntotal = 0;
+    for (int i = 0; i < count; ++i) ntotal += projs[i].N;
+    kernel = auto_kernel(M, ntotal, K);
+  }
   if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
   if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -403,7 +421,7 @@ size_t rf_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     dev.gfx950 = false;
   }
   const int n32 = (int)N;
-  size_t extra = rf::gemm_workspace_bytes(rf::plan_gemm((int)M, &n32, 1, (int)K, dev));
+  size_t extra = rf::gemm_workspace_bytes(rf::plan_gemm((int)M, &n32, 1, (int)K, dev, true));
   if (M <= 64) {
     const rf::GemvPlan p = rf::plan_gemv_int4((int)M, n32, (int)K, dev);
     const size_t g = rf::gemv_workspace_bytes(p, (int)M, &n32, 1);
@@ -431,7 +449,7 @@ int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void
   if (st != RF_W8A16_OK) return st;
   if (!dev.gfx950) return RF_W8A16_EDEVICE;
 
-  if (kernel == RF_W8A16_KERNEL_AUTO) kernel = auto_kernel(M);
+  if (kernel == RF_W8A16_KERNEL_AUTO) kernel = auto_kernel_int4(M);
   if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
   if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -463,7 +481,7 @@ int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void
       return RF_W8A16_EWORKSPACE;
     e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);
   } else {
-    const rf::GemmPlan p = rf::plan_gemm(pr.M, &n32, 1, pr.K, dev);
+    const rf::GemmPlan p = rf::plan_gemm(pr.M, &n32, 1, pr.K, dev, true);
     if (p.splits > 1 && !workspace_ok(rf::gemm_workspace_bytes(p))) return RF_W8A16_EWORKSPACE;
     e = rf::launch_gemm(pr, p, p.splits > 1 ? workspace : nullptr, s);
   }

@@ -617,12 +617,15 @@ enum GemmCfgId {
   kV3M64N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: small M
   kV3M256N256,    // 8 wavefronts 2x4, 2 stages, 1 workgroup/CU: whole rounds of big tiles
   kDmaM128N128,   // 64-bit addresses: when the v3 32-bit offsets could overflow
+  kV3M32N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 17..32, with K splits
+  kV3M64N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 33..64, with K splits
   kGemmCfgCount
 };
 
 // {BM, BN, workgroups per CU}
 constexpr int kGemmTile[kGemmCfgCount][3] = {{128, 256, 2}, {128, 128, 3}, {128, 128, 2},
-                                             {64, 256, 2},  {256, 256, 1}, {128, 128, 1}};
+                                             {64, 256, 2},  {256, 256, 1}, {128, 128, 1},
+                                             {32, 64, 4},   {64, 64, 4}};
 
 namespace {
 
@@ -657,8 +660,27 @@ void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
 // tables (src/ops/rpu_linear_tiling.h:69-127, selectors :544-595), as rules
 // over (M, total N) tuned on MI355X, plus a K split when the output has
 // fewer tiles than the chip has workgroup slots.
-GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev) {
+//
+// M <= 64 (int8): small tiles (32x64 or 64x64, four per CU) and a K split
+// that brings the launch to about three workgroups per CU -- the largest
+// power of two <= 768 / tiles, at most 8, each split at least 8 K blocks
+// (measured on the Qwen3-8B / Qwen3-VL-32B shapes at M 32..64; with the
+// 64x256 tile these launches had 16..100 workgroups).
+GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev, bool int4) {
   const int cus = dev.cus > 0 ? dev.cus : 256;
+  if (M <= 64 && !int4) {
+    GemmPlan p;
+    p.cfg = M <= 32 ? kV3M32N64 : kV3M64N64;
+    set_tiles(p, M, Ns, nproj);
+    const int kblocks = (int)ceil_div(K, 64);
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    int s = 1;
+    while (s < 8 && (int64_t)(2 * s) * tiles <= 3LL * cus && kblocks / (2 * s) >= 8) s *= 2;
+    if (tiles > kMaxSplitTiles) s = 1;
+    p.kb_per_split = (int)ceil_div(kblocks, s);
+    p.splits = (int)ceil_div(kblocks, p.kb_per_split);
+    return p;
+  }
   int64_t ntotal = 0, t256 = 0;
   for (int i = 0; i < nproj; ++i) {
     ntotal += Ns[i];
@@ -773,6 +795,8 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
     case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2>(ka, stream);
     case kV3M256N256: return launch_v3_t<256, 256, 2, 4, 2, 1>(ka, stream);
     case kDmaM128N128: return launch_dma_t<128, 128, 1, 4, 3>(ka, stream);
+    case kV3M32N64: return launch_v3_t<32, 64, 1, 4, 4, 4>(ka, stream);
+    case kV3M64N64: return launch_v3_t<64, 64, 1, 4, 4, 4>(ka, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -63,7 +63,9 @@ struct DeviceInfo {
 int device_info(DeviceInfo* out);
 
 GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev);
-GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev);
+// int4: packed-int4 weights (TILE16X128_I4) take the large-tile rules only.
+GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
+                   bool int4 = false);
 // GEMV plan of a packed-int4 weight (one projection).
 GemvPlan plan_gemv_int4(int M, int N, int K, const DeviceInfo& dev);
 // Workspace bytes past the RF_W8A16_WS_COUNTER_BYTES counter region.

@@ -189,7 +189,15 @@ def test_workspace_bytes_multi_matches_single():
 def test_select_kernel_policy():
     assert rf.select_kernel(1, 4096, 4096) == rf.KERNEL_GEMV
     assert rf.select_kernel(16, 151936, 5120) == rf.KERNEL_GEMV
-    assert rf.select_kernel(64, 4096, 4096) == rf.KERNEL_GEMV
+    # M 17..28: the GEMV only for small weights (N*K <= 2^24)
+    assert rf.select_kernel(17, 4096, 4096) == rf.KERNEL_GEMV
+    assert rf.select_kernel(28, 4096, 4096) == rf.KERNEL_GEMV
+    assert rf.select_kernel(17, 8192, 5120) == rf.KERNEL_GEMM
+    assert rf.select_kernel(29, 4096, 4096) == rf.KERNEL_GEMM
+    assert rf.select_kernel(32, 1024, 5120) == rf.KERNEL_GEMV   # N*K <= 2^23
+    assert rf.select_kernel(33, 1024, 5120) == rf.KERNEL_GEMM
+    assert rf.select_kernel(32, 5120, 25600) == rf.KERNEL_GEMM
+    assert rf.select_kernel(64, 4096, 4096) == rf.KERNEL_GEMM
     assert rf.select_kernel(65, 4096, 4096) == rf.KERNEL_GEMM
     assert rf.select_kernel(2048, 12288, 4096) == rf.KERNEL_GEMM
     with pytest.raises(RuntimeError):
