@@ -822,7 +822,16 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   const int cu = dev.cus > 0 ? dev.cus : 256;
   auto strips_ge = [&](int n256) { return (int64_t)nstrips * 256 >= (int64_t)n256 * cu; };
   int cfg, splits = 1;
-  if (M <= 4) {
+  if (M <= 16 && !strips_ge(640) && kblocks >= 256) {
+    // Very long K (>= 16384) on few strips (Qwen3-VL-32B down_proj): two
+    // strips per 8-wavefront workgroup and an 8-way K split.
+    cfg = kG1x2W8U2;
+    splits = 8;
+  } else if (M <= 4 && strips_ge(257) && !strips_ge(640) && kblocks >= 80) {
+    // Long K (>= 5120) on 257..639 strips (Qwen3-VL-32B q_proj, o_proj):
+    // x in LDS at M <= 2, two strips per workgroup at M 3..4.
+    cfg = (M <= 2 && lds_fits(kG1x1W8U4XL, M, kblocks)) ? kG1x1W8U4XL : kG1x2W8U2;
+  } else if (M <= 4) {
     // x staged in LDS (one DMA copy per workgroup instead of every
     // wavefront re-reading the same L2 lines) pays off at M <= 2.
     if (strips_ge(640)) {
@@ -843,8 +852,10 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
       cfg = kG1x4W4U2;
     } else if (strips_ge(1024)) {
       cfg = kG1x2W8U2;
-    } else if (strips_ge(512)) {
+    } else if (strips_ge(640)) {
       cfg = kG1x4W8U2;
+    } else if (strips_ge(512)) {
+      cfg = kG1x2W8U2;  // 512..639 strips: four per workgroup leaves half the CUs idle
     } else if (strips_ge(257)) {
       cfg = kG1x2W16U2;
     } else if (kblocks >= 128) {

@@ -389,11 +389,16 @@ GEMV_POLICY = [
     (1, 512, 1024),    # M<=4, default (short K, or M > 1)
     (8, 32768, 128),   # M 5..16, >=2048 strips
     (16, 16384, 256),  # M 5..16, >=1024 strips: two strips per 8-wave workgroup
-    (12, 8192, 256),   # M 5..16, >=512 strips
+    (12, 10240, 256),  # M 5..16, 640..1023 strips: 4 strips per WG
     (10, 5000, 512),   # M 5..16, 257..511 strips: two strips per 16-wave workgroup
     (16, 1024, 8192),  # M 5..16, long K: 4-way K split
     (9, 1000, 1024),   # M 5..16, <=64 strips: 4-way K split
     (16, 2048, 1024),  # M 5..16, default
+    (1, 5120, 16384),  # M <= 16, < 640 strips, K >= 16384: 2 strips per WG, 8-way split
+    (16, 4112, 16456), # the same at M 16, ragged N and K
+    (1, 8192, 5120),   # M <= 2, 257..639 strips, K >= 5120: x in LDS
+    (4, 5120, 8192),   # M 3..4, the same strips and K: 2 strips per WG
+    (12, 8192, 512),   # M 5..16, 512..639 strips: 2 strips per WG
     (20, 16384, 128),  # M 17..32, >=1024 strips
     (32, 640, 8192),   # M 17..32, long K: 4-way K split
     (17, 1024, 512),   # M 17..32, <=64 strips: 4-way K split
