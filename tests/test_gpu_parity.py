@@ -579,11 +579,13 @@ def test_op_errors_on_device():
         rf.linear(_to_dev(x), packed, sd, torch.zeros(39, dtype=torch.float16, device=DEV))
 
 
-@pytest.mark.parametrize("m,n,k", [(16, 1024, 8192), (1, 4096, 1024), (300, 384, 1024)])
+@pytest.mark.parametrize("m,n,k", [(16, 1024, 8192), (1, 4096, 1024), (300, 384, 1024),
+                                   (48, 5120, 8192)])
 def test_graph_capture_replays_match_eager(m, n, k):
     """The op inside a HIP graph: every replay (with eager work between replays)
     equals the eager result bit for bit.  (16, 1024, 8192) takes the split-K
-    GEMV path, whose counters must be left zeroed for the next replay."""
+    GEMV path and (48, 5120, 8192) the 8-way split mid-M GEMM, whose counters
+    must be left zeroed for the next replay."""
     _say(f"graph capture M={m} N={n} K={k}")
     x, q, s, b = make_case(m, n, k, seed=17, bias=True)
     xd, packed, sd, bd = _to_dev(x), rf.pack_weight(_to_dev(q)), _to_dev(s), _to_dev(b)

@@ -166,3 +166,29 @@ def test_w4a16_capi_direct_call():
     torch.cuda.synchronize()
     assert st == capi.OK, capi.status_str(st)
     check(y.cpu().numpy(), x, q, s, label="capi direct")
+
+
+@pytest.mark.parametrize("m,n,k,gs", [(16, 1024, 8192, 32), (300, 1024, 8192, 0)])
+def test_w4a16_graph_replays_match_eager(m, n, k, gs):
+    """Inside a HIP graph: split-K GEMV (16 rows) and split-K GEMM (300 rows)
+    replays, with eager calls between them, equal the eager result bit for bit."""
+    q, s = make_w4(n, k, gs, 6)
+    x = o8.make_activation(7, m, k)
+    xd, sd, wp = _dev(x), _dev(s), rf.pack_weight_int4(_dev(q))
+    eager = rf.linear_w4a16(xd, wp, sd)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        rf.linear_w4a16(xd, wp, sd)  # warm-up: workspace for this stream
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        out = rf.linear_w4a16(xd, wp, sd)
+    for i in range(4):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        assert torch.equal(rf.linear_w4a16(xd, wp, sd), eager)
+    check(out.cpu().numpy(), x, q, s, label=f"w4 graph {m}x{n}x{k} gs={gs}")
