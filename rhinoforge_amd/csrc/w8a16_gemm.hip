@@ -200,7 +200,14 @@ __device__ __forceinline__ void store_tile(const TileTarget& t, const floatx4 (&
 // of the int8 path (so the A operand path is shared unchanged).  Group-wise
 // int4 also copies the block's scale rows ([K/gs][N], BN columns; one row,
 // or two for gs = 32) into LDS, by wavefront 0, and scales at dequantization.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8>
+//
+// IL (int8 only): both K steps' A fragments of a block are read up front, the
+// second step's reads are interleaved one per MFMA with the first step's
+// MFMAs (sched_group_barrier), and the wavefront runs its MFMA section at
+// raised issue priority (s_setprio 1).  Same arithmetic in the same order;
+// chosen where two wavefronts per SIMD are resident (see plan_gemm).
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8,
+          bool IL = false>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(OCC * WAVES_M * WAVES_N / 4, 8)))
 void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
@@ -284,10 +291,11 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)smem;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   // Local K block i of this split = global K block kb0 + i, LDS stage i % STAGES.
-  auto issue = [&](int i) {
+  // may_tail = false (a constant at every call site) drops the K-tail check.
+  auto issue = [&](int i, bool may_tail) {
     const int kb = kb0 + i;
     const uint32_t st = lds0 + (i % STAGES) * STAGE;
-    if (k_tail && kb == a.kblocks - 1) {
+    if (may_tail && k_tail && kb == a.kblocks - 1) {
       // Last block with columns past K: those chunks load column 0 instead
       // and are zeroed after they land (fix_tail).
 #pragma unroll
@@ -355,6 +363,35 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
           for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(af[r], b, acc[r][j]);
         }
       }
+    } else if constexpr (IL) {
+      __builtin_amdgcn_s_setprio(1);
+      uint4 braw[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        braw[j] = *reinterpret_cast<const uint4*>(st + A_BYTES + (wn * TN + j) * kTileBytes + lane * 16);
+      half8 af0[TM], af1[TM];
+#pragma unroll
+      for (int r = 0; r < TM; ++r) af0[r] = *reinterpret_cast<const half8*>(st + aoff0 + r * 16 * 128);
+#pragma unroll
+      for (int r = 0; r < TM; ++r) af1[r] = *reinterpret_cast<const half8*>(st + aoff1 + r * 16 * 128);
+#pragma unroll
+      for (int step = 0; step < 2; ++step)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const half8 b = step == 0 ? dequant8(braw[j].x, braw[j].y) : dequant8(braw[j].z, braw[j].w);
+#pragma unroll
+          for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(step == 0 ? af0[r] : af1[r], b, acc[r][j]);
+        }
+      // Masks: 0x100 LDS reads, 0x008 MFMA.  The B and first-step A reads
+      // go first, then each second-step A read follows one MFMA.
+      __builtin_amdgcn_sched_group_barrier(0x100, TN + TM, 0);
+#pragma unroll
+      for (int r = 0; r < TM; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * TM * TN - TM, 0);
+      __builtin_amdgcn_s_setprio(0);
     } else {
       uint4 braw[TN];
 #pragma unroll
@@ -378,10 +415,31 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
 
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < nk) issue(s);
+    if (s < nk) issue(s, true);
   // Group-wise int4: wavefront 0 issues one more DMA per K block (scale rows).
   const bool extra = GS && wave_u == 0;
-  for (int i = 0; i < nk; ++i) {
+  // Steady state: the block issued (i + STAGES - 1 <= nk - 2) is never the
+  // last one, so it holds no K tail, and STAGES - 2 blocks stay in flight
+  // after block i; the loop carries no tail checks (their branches cost
+  // about 4% on a 12288-deep K).
+  int i = 0;
+  for (; i < nk - STAGES; ++i) {
+    if constexpr (STAGES - 2 >= 2) {
+      if (extra) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (LOADS + 1)) : "memory");
+      else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LOADS) : "memory");
+    } else if constexpr (STAGES - 2 == 1) {
+      if (extra) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS + 1) : "memory");
+      else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS) : "memory");
+    } else {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    barrier_lds();
+    issue(i + STAGES - 1, false);
+    compute(i);
+  }
+  // The last STAGES blocks (or all of a short split): the block issued may be
+  // the K tail, and fewer blocks remain in flight.
+  for (; i < nk; ++i) {
     const int ahead = min(STAGES - 2, nk - 1 - i);  // blocks issued after i
     if (ahead >= 2) {
       if (extra) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (LOADS + 1)) : "memory");
@@ -395,7 +453,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     if (k_tail && kb0 + i == a.kblocks - 1) fix_tail(i);
     barrier_lds();
     // Everyone is past compute(i-1): its stage can be refilled.
-    if (i + STAGES - 1 < nk) issue(i + STAGES - 1);
+    if (i + STAGES - 1 < nk) issue(i + STAGES - 1, true);
     compute(i);
   }
 
@@ -586,13 +644,15 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(
   store_tile<TM, TN>(tt, acc, m0 + wm * WM, (strip0 + wn * TN) * 16, lane, a.M, full);
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8,
+          bool IL = false>
 hipError_t launch_v3_t(const GemmKernelArgs& ka, hipStream_t stream) {
+  static_assert(!IL || WF == kWfInt8, "the interleaved schedule is an int8 variant");
   const int64_t tiles = (int64_t)ka.tiles_m * ka.tiles_n;
   if (tiles <= 0 || tiles > 0x7fffffff || ka.splits < 1 || ka.splits > 65535 ||
       !v3_offsets_fit(ka, BM, BN))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, WF>),
+  hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, WF, IL>),
                      dim3((unsigned)tiles, (unsigned)ka.splits), dim3(WAVES_M * WAVES_N * 64), 0,
                      stream, ka);
   return hipGetLastError();
@@ -619,13 +679,14 @@ enum GemmCfgId {
   kDmaM128N128,   // 64-bit addresses: when the v3 32-bit offsets could overflow
   kV3M32N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 17..32, with K splits
   kV3M64N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 33..64, with K splits
+  kV3M128N128IL,  // kV3M128N128 with the interleaved MFMA schedule (int8): 1..2 tiles per CU
   kGemmCfgCount
 };
 
 // {BM, BN, workgroups per CU}
 constexpr int kGemmTile[kGemmCfgCount][3] = {{128, 256, 2}, {128, 128, 3}, {128, 128, 2},
                                              {64, 256, 2},  {256, 256, 1}, {128, 128, 1},
-                                             {32, 64, 4},   {64, 64, 4}};
+                                             {32, 64, 4},   {64, 64, 4},   {128, 128, 3}};
 
 namespace {
 
@@ -714,6 +775,12 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
       p.splits = (int)ceil_div(kblocks, p.kb_per_split);  // no empty split
     }
   }
+  // 128x128 tiles that leave one to two workgroups (two wavefronts per SIMD)
+  // on a CU: the interleaved schedule (+8..16% on 384 and 512 tiles of
+  // M 1024..4096, K 4096..12288; -1..3% at one tile per CU or 2.5..3 per CU,
+  // where the plain schedule stays).
+  if (!int4 && p.cfg == kV3M128N128 && p.splits == 1 && tiles > cus && tiles <= 2LL * cus)
+    p.cfg = kV3M128N128IL;
   return p;
 }
 
@@ -797,6 +864,7 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
     case kDmaM128N128: return launch_dma_t<128, 128, 1, 4, 3>(ka, stream);
     case kV3M32N64: return launch_v3_t<32, 64, 1, 4, 4, 4>(ka, stream);
     case kV3M64N64: return launch_v3_t<64, 64, 1, 4, 4, 4>(ka, stream);
+    case kV3M128N128IL: return launch_v3_t<128, 128, 1, 4, 2, 3, kWfInt8, true>(ka, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -428,6 +428,7 @@ GEMM_POLICY = [
     (100, 520, 1032),    # M < 128: 64x256 tiles
     (1024, 8200, 264),   # M >= 1024, N >= 8192: 128x256 tiles, 2 workgroups/CU
     (1100, 1000, 520),   # M >= 1024, N < 8192: 128x128 tiles, 3 workgroups/CU
+    (1300, 3900, 1032),  # the same with 341 tiles (1..2 per CU): interleaved schedule, ragged M/N/K
     (1024, 16384, 128),  # M >= 1024, 256x256 tiles fill whole rounds (4 x 64 = 256)
     (1025, 65300, 72),   # the same rule on ragged M, N, K (5 x 256 = 1280 tiles)
     (200, 16400, 136),   # 128 <= M < 1024, N >= 16384: 128x256 tiles
