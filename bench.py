@@ -33,6 +33,9 @@ The same JSON line carries
   * configs       -- per-launch timings of configs 0, 2 and 4 and of each
                      config-1 projection (back-to-back launches on rotating
                      weight copies);
+  * read_envelope -- the same 12-launch step with a plain streaming read of
+                     the same bytes in place of the GEMV (lib/librf_bench.so):
+                     the bound the launch structure itself puts on `value`;
   * cpu_baseline  -- the CPU restatement of the reference's dequantize-then-
                      matmul path (oracle, numpy/BLAS on the host cores) on a
                      bounded sample of config 1 at M=1.
@@ -227,6 +230,54 @@ def bench_decode(torch, rf, steps, warmup):
         "per_M_GBps": per_m,
         "per_launch": rows,
     }
+
+
+def read_envelope(torch, steps, warmup):
+    """The decode step's launch structure with the GEMV replaced by a plain
+    streaming read (lib/librf_bench.so): 12 launches per step reading the
+    same algorithmic byte counts, rotated over LAYER_COPIES buffer sets, eager
+    on one stream and timed like the GEMV step.  Launch gaps, ramp-up and
+    drain bound the decode step no matter what kernel runs; this is that
+    bound on the device at hand."""
+    import ctypes
+    path = os.path.join(ROOT, "rhinoforge_amd", "lib", "librf_bench.so")
+    if not os.path.isfile(path):
+        log(f"read envelope skipped: {path} not built")
+        return None
+    lib = ctypes.CDLL(path)
+    lib.rf_bench_stream_read.restype = ctypes.c_int
+    lib.rf_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                         ctypes.c_void_p]
+    sizes = []  # algorithmic bytes of the fused step's launches, in launch order
+    for m in DECODE_M:
+        for idxs in ((0, 1, 2), (3,), (4, 5), (6,)):
+            k = QWEN3_8B[idxs[0]][2]
+            b = sum(nbytes(m, QWEN3_8B[i][1], k) - 2 * m * k for i in idxs) + 2 * m * k
+            sizes.append((b + 15) // 16 * 16)
+    bufs = [[torch.empty(b, dtype=torch.uint8, device="cuda") for b in sizes]
+            for _ in range(LAYER_COPIES)]
+    for c in bufs:
+        for t in c:
+            t.fill_(1)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        for s, b in enumerate(sizes):
+            buf = bufs[(i * len(DECODE_M) + s // 4) % LAYER_COPIES][s]
+            st = lib.rf_bench_stream_read(buf.data_ptr(), b, sink.data_ptr(), stream)
+            if st != 0:
+                raise RuntimeError(f"rf_bench_stream_read: hipError {st}")
+
+    for i in range(warmup):
+        step(i)
+    with Timer(torch) as t:
+        for i in range(steps):
+            step(warmup + i)
+    del bufs
+    torch.cuda.empty_cache()
+    gbps = sum(sizes) * steps / (t.ms * 1e-3) / 1e9
+    return {"GBps": gbps, "ms_per_step": t.ms / steps, "launches_per_step": len(sizes)}
 
 
 def settle(torch, step, seconds, min_steps):
@@ -517,6 +568,9 @@ def main():
     dec = bench_decode(torch, rf, args.steps, args.warmup)
     log(f"decode: {dec['GBps']:.1f} GB/s ({dec['avg_launch_us']:.2f} us/launch, q/k/v and "
         f"gate/up fused); one launch per projection: {dec['per_op_GBps']:.1f} GB/s")
+    env = read_envelope(torch, args.steps, args.warmup)
+    if env:
+        log(f"read envelope of the same 12 launches: {env['GBps']:.1f} GB/s")
     pre = None
     if not args.no_prefill:
         log("prefill (cfg3)...")
@@ -588,6 +642,15 @@ def main():
                          "avg_launch_us": round(pre["avg_launch_us"], 2),
                          "flops_per_launch": pre["flops_per_launch"]},
             "per_launch": pre["per_launch"],
+        },
+        "read_envelope": None if env is None else {
+            "GBps": round(env["GBps"], 1),
+            "frac_of_peak": round(env["GBps"] / HBM_PEAK_GBS, 4),
+            "value_over_envelope": round(dec["GBps"] / env["GBps"], 4),
+            "ms_per_step": round(env["ms_per_step"], 4),
+            "what": ("the decode step's 12 launches with the GEMV replaced by a plain "
+                     "non-temporal streaming read of the same byte counts (rotated buffers, "
+                     "eager, same stream and timer): the rate this launch structure allows"),
         },
         "cpu_baseline": cpu,
         "decode_per_launch": dec["per_launch"],

@@ -3,6 +3,8 @@
 * ``lib/librf_w8a16.so``       -- gfx950 HIP kernels + the C ABI (hipcc)
 * ``lib/librf_w8a16_torch.so`` -- the thin torch-library op (g++ against
   the installed PyTorch-ROCm headers), linked to the C-ABI library
+* ``lib/librf_bench.so``       -- bench.py's streaming-read reference kernel
+  (a measurement helper, not part of the C ABI)
 
 Every HIP translation unit is compiled with packed-FP32 VALU ops disabled
 (``-Xclang -target-feature -Xclang -packed-fp32-ops``); the host pass warns
@@ -26,6 +28,7 @@ INCLUDE = ROOT / "include"
 CAPI_SOURCES = ["w8a16_capi.hip", "w8a16_gemv.hip", "w8a16_gemm.hip"]
 CAPI_LIB = LIBDIR / "librf_w8a16.so"
 TORCH_LIB = LIBDIR / "librf_w8a16_torch.so"
+BENCH_LIB = LIBDIR / "librf_bench.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 OFFLOAD_ARCH = "gfx950"
@@ -104,9 +107,20 @@ def build_torch_op(verbose: bool = False) -> Path:
     return TORCH_LIB
 
 
+def build_bench(verbose: bool = False) -> Path:
+    """Compile bench.py's streaming-read helper into lib/librf_bench.so."""
+    LIBDIR.mkdir(exist_ok=True)
+    tmp = BENCH_LIB.with_name(BENCH_LIB.name + f".tmp{os.getpid()}")
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "bench_read.hip"),
+          "-Wl,-soname,librf_bench.so", "-o", str(tmp)], verbose)
+    _atomic_link(tmp, BENCH_LIB)
+    return BENCH_LIB
+
+
 def build_all(verbose: bool = False) -> None:
     build_capi(verbose)
     build_torch_op(verbose)
+    build_bench(verbose)
 
 
 if __name__ == "__main__":
