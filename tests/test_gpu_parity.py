@@ -667,6 +667,33 @@ def test_linear_multi_gemm_one_launch_ragged_split():
         assert rep.ok, f"multi gemm vs single: {rep}"
 
 
+def test_linear_multi_gemm_whole_rounds_two_projections():
+    """M=1024, gate/up-like pair N = 8200 (ragged) and 7936, K = 520 (K tail):
+    4 x (33 + 31) = 256 tiles of 256x256 would fill one whole round, the case
+    where a single matrix takes 256x256 tiles and a multi-projection launch
+    128x256.  Each output against the oracle and against a single call."""
+    m, k = 1024, 520
+    ns = [(8200, True), (7936, False)]
+    x = o.make_activation(o.derive_seed(26, "x", m, k), m, k)
+    rows = np.random.default_rng(26).choice(m, 96, replace=False)
+    cases = []
+    for pi, (n, has_bias) in enumerate(ns):
+        q, s = make_weights(n, k, seed=260 + pi)
+        b = (o.normal(o.derive_seed(27, "b", n, pi), (n,)) * 0.1).astype(np.float16) if has_bias else None
+        cases.append((q, s, b, rf.pack_weight(_to_dev(q))))
+    xd = _to_dev(x)
+    _say(f"linear_multi gemm whole rounds M={m} K={k} Ns={[n for n, _ in ns]}")
+    ys = rf.linear_multi(xd, [c[3] for c in cases], [_to_dev(c[1]) for c in cases],
+                         [None if c[2] is None else _to_dev(c[2]) for c in cases])
+    torch.cuda.synchronize()
+    for pi, (q, s, b, packed) in enumerate(cases):
+        y = ys[pi].cpu().numpy()
+        assert_parity(y, x, q, s, b, rows=rows, label=f"multi gemm whole rounds p{pi}")
+        single = rf.linear(xd, packed, _to_dev(s), None if b is None else _to_dev(b)).cpu().numpy()
+        rep = o.check_tolerance(y[rows], single[rows], o.oracle_fp64(x[rows], q, s, b))
+        assert rep.ok, f"multi gemm whole rounds vs single: {rep}"
+
+
 def test_linear_multi_split_k_and_capi():
     """M=16, K=12288: the shared launch takes the 4-way K split; also via ctypes."""
     m, k = 16, 12288
