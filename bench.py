@@ -375,8 +375,10 @@ def bench_other_configs(torch, rf):
     out["cfg2_lm_head"] = rows
     del head
     torch.cuda.empty_cache()
-    # cfg4: Qwen3-VL-32B projections at M in {1, 32, 512}, two layer copies (980 MB)
-    copies = [make_layer(torch, rf, QWEN3_VL_32B, seed=940 + c) for c in range(2)]
+    # cfg4: Qwen3-VL-32B projections at M in {1, 32, 512}, four layer copies (1.96 GB):
+    # every projection's copies together exceed the 256 MB Infinity Cache (two
+    # copies of a 131 MB gate/up/down weight would mostly be served from it)
+    copies = [make_layer(torch, rf, QWEN3_VL_32B, seed=940 + c) for c in range(4)]
     rows = []
     for m in (1, 32, 512):
         x = torch.randn(m, 25600, device="cuda").half()

@@ -731,9 +731,26 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   const int cus = dev.cus > 0 ? dev.cus : 256;
   if (M <= 64 && !int4) {
     GemmPlan p;
+    const int kblocks = (int)ceil_div(K, 64);
+    // Wide launches: every workgroup reads its M x K activation panel, so the
+    // activation traffic is (tile columns) x M x K x 2 bytes -- as large as
+    // the weights themselves with 64-column tiles at N = 51200.  64x256 tiles
+    // read it a quarter as often: taken when they alone give >= 0.75
+    // workgroups per CU, or from M = 33 with a 2-way K split at >= 0.375
+    // (Qwen3-VL-32B gate/up at M 32..64: 52..57 us instead of 63..84 us;
+    // Qwen3-8B gate/up at M 48..64: 28.5 instead of 30.5..32 us; MI355X).
+    int64_t w256 = 0;
+    for (int i = 0; i < nproj; ++i) w256 += ceil_div(Ns[i], 256);
+    const bool wide = w256 * 4 >= 3LL * cus;
+    if (wide || (M > 32 && w256 * 8 >= 3LL * cus && kblocks >= 2 * kMinKbPerSplit)) {
+      p.cfg = kV3M64N256;
+      set_tiles(p, M, Ns, nproj);
+      p.kb_per_split = wide ? kblocks : (int)ceil_div(kblocks, 2);
+      p.splits = (int)ceil_div(kblocks, p.kb_per_split);
+      return p;
+    }
     p.cfg = M <= 32 ? kV3M32N64 : kV3M64N64;
     set_tiles(p, M, Ns, nproj);
-    const int kblocks = (int)ceil_div(K, 64);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     int s = 1;
     while (s < 8 && (int64_t)(2 * s) * tiles <= 3LL * cus && kblocks / (2 * s) >= 8) s *= 2;

@@ -440,7 +440,8 @@ GEMM_POLICY = [
     # M <= 64: 32x64 / 64x64 tiles, split to ~3 workgroups per CU
     (20, 4096, 4096),    # M 17..32: 64 tiles, 8-way split (8 K blocks each)
     (48, 5120, 8192),    # M 33..64: 80 tiles, 8-way split
-    (40, 25600, 5120),   # 400 tiles: no split
+    (40, 25600, 5120),   # M 33..64, 100 tiles of 64x256 (>= 96): 64x256 with a 2-way K split
+    (24, 49408, 136),    # 193 tiles of 64x256 (>= 192): 64x256, no split; ragged N, K tail
     (64, 1000, 200),     # ragged N, 4 K blocks: no split
     (33, 4104, 520),     # ragged M and N, K tail (9 K blocks): no split
     (17, 2056, 1544),    # 33 tiles, 25 K blocks: 2-way split, K tail in split 1
