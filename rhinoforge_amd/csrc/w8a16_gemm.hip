@@ -786,7 +786,10 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   const int64_t slots = (int64_t)cus * kGemmTile[p.cfg][2];
   p.splits = 1;
   p.kb_per_split = kblocks;
-  if (tiles < slots && tiles <= kMaxSplitTiles) {
+  // K split only below one tile per CU: at one to two per CU the split's
+  // partial round trip costs more than the extra workgroups gain (M = 512,
+  // 256 tiles of 128x128: 44 us unsplit, 50 us with two splits).
+  if (tiles < cus && tiles <= kMaxSplitTiles) {
     int s = (int)(slots / tiles);
     s = s < kMaxGemmSplits ? s : kMaxGemmSplits;
     s = s < kblocks / kMinKbPerSplit ? s : kblocks / kMinKbPerSplit;
@@ -797,9 +800,11 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   }
   // 128x128 tiles that leave one to two workgroups (two wavefronts per SIMD)
   // on a CU: the interleaved schedule (+8..16% on 384 and 512 tiles of
-  // M 1024..4096, K 4096..12288; -1..3% at one tile per CU or 2.5..3 per CU,
-  // where the plain schedule stays).
-  if (!int4 && p.cfg == kV3M128N128 && p.splits == 1 && tiles > cus && tiles <= 2LL * cus)
+  // M 1024..4096, K 4096..12288, and +20% on the fused Qwen3-VL-32B q/k/v at
+  // M = 512; -1..3% at one tile per CU or 2.5..3 per CU, where the plain
+  // schedule stays).
+  if (!int4 && (p.cfg == kV3M128N128 || p.cfg == kV3M128N128S3) && p.splits == 1 && tiles > cus &&
+      tiles <= 2LL * cus)
     p.cfg = kV3M128N128IL;
   return p;
 }

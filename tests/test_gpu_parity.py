@@ -434,6 +434,8 @@ GEMM_POLICY = [
     (200, 16400, 136),   # 128 <= M < 1024, N >= 16384: 128x256 tiles
     (300, 384, 1024),    # 128 <= M < 1024, N < 16384: 128x128 tiles, 3 stages
     (300, 384, 4096),    # 9 tiles, 64 K blocks: 4-way K split of 16 blocks
+    (512, 4096, 1032),   # 128 <= M < 1024: 256 tiles (one per CU), no K split; K tail
+    (640, 7000, 520),    # 128 <= M < 1024: 275 tiles (1..2 per CU), interleaved schedule
     (200, 1000, 2056),   # 16 tiles, 33 K blocks: 2-way split, K tail in split 1
     (100, 520, 4096),    # M < 128: 6 tiles, 4-way K split
     (1024, 2048, 8192),  # M >= 1024: 128 tiles of 128x128, 6-way K split
