@@ -759,24 +759,41 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     p.splits = (int)ceil_div(kblocks, p.kb_per_split);
     return p;
   }
-  int64_t ntotal = 0, t256 = 0;
+  int64_t ntotal = 0, cols256 = 0, cols128 = 0;  // tile columns 256 and 128 wide
   for (int i = 0; i < nproj; ++i) {
     ntotal += Ns[i];
-    t256 += ceil_div(Ns[i], 256);
+    cols256 += ceil_div(Ns[i], 256);
+    cols128 += ceil_div(Ns[i], 128);
   }
-  t256 *= ceil_div(M, 256);
+  const int64_t t256 = ceil_div(M, 256) * cols256;         // 256x256 tiles
+  const int64_t t128x256 = ceil_div(M, 128) * cols256;     // 128x256 tiles
+  const int64_t t128 = ceil_div(M, 128) * cols128;         // 128x128 tiles
   GemmPlan p;
   if (M < 128) {
     p.cfg = kV3M64N256;
-  } else if (M >= 1024) {
+  } else if (M >= 1024 && (t256 % cus == 0 || t256 >= 4 * cus) && nproj == 1) {
     // 256x256 tiles only when they fill whole rounds of the chip (or many
     // rounds): at 1.5 rounds the half-empty last round costs more than the
     // bigger tile gains.  A launch of several projections (gate/up) keeps
     // 128x256: measured 0.5..2% faster on the fused gate/up at M 2048 and
     // 4096 (and 1..2% inside the MLP step), where one weight matrix of the
     // same shape runs 2..9% faster with 256x256.
-    if ((t256 % cus == 0 || t256 >= 4 * cus) && nproj == 1) p.cfg = kV3M256N256;
-    else p.cfg = ntotal >= 8192 ? kV3M128N256 : kV3M128N128;
+    p.cfg = kV3M256N256;
+  } else if (!int4 && t128 <= 6LL * cus) {
+    // Up to six 128x128 tiles per CU the tiles a CU gets decide the time:
+    // a launch takes ceil(tiles / CUs) tile times, a 128x256 tile costing
+    // two 128x128 ones.  The cheaper shape wins; on a tie 128x128 when it
+    // lands one to two tiles per CU (the interleaved schedule below), else
+    // 128x256.  (Measured over the Qwen3-8B and Qwen3-VL-32B projections at
+    // M 128..4096 on MI355X: e.g. fused q/k/v 10240 x 5120 at M 1024 / 2048
+    // 100.6 / 171 us instead of 110.5 / 187 us with 128x256, gate/up
+    // 24576 x 4096 at M 512 93.9 instead of 99.7 us.)
+    const int64_t r256 = ceil_div(t128x256, cus) * 2, r128 = ceil_div(t128, cus);
+    const bool use128 = r128 < r256 || (r128 == r256 && t128 > cus && t128 <= 2LL * cus);
+    p.cfg = !use128 ? kV3M128N256
+                    : (M < 1024 && t128 <= 2LL * cus) ? kV3M128N128S3 : kV3M128N128;
+  } else if (M >= 1024) {
+    p.cfg = ntotal >= 8192 ? kV3M128N256 : kV3M128N128;
   } else {
     p.cfg = ntotal >= 16384 ? kV3M128N256 : kV3M128N128S3;
   }
@@ -786,17 +803,30 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   const int64_t slots = (int64_t)cus * kGemmTile[p.cfg][2];
   p.splits = 1;
   p.kb_per_split = kblocks;
-  // K split only below one tile per CU: at one to two per CU the split's
-  // partial round trip costs more than the extra workgroups gain (M = 512,
-  // 256 tiles of 128x128: 44 us unsplit, 50 us with two splits).
+  int s = 1;
   if (tiles < cus && tiles <= kMaxSplitTiles) {
-    int s = (int)(slots / tiles);
+    // Below one tile per CU: split K up to the chip's workgroup slots, each
+    // split keeping >= 16 K blocks while the launch has at most one
+    // workgroup per CU and >= 24 beyond that (shorter splits cost more in
+    // partial round trips than they gain: 512 x 4096 x 4096, 128 tiles:
+    // 26.5 us with 2 splits, 28.6 us with 4).
+    s = (int)(slots / tiles);
     s = s < kMaxGemmSplits ? s : kMaxGemmSplits;
-    s = s < kblocks / kMinKbPerSplit ? s : kblocks / kMinKbPerSplit;
-    if (s >= 2) {
-      p.kb_per_split = (int)ceil_div(kblocks, s);
-      p.splits = (int)ceil_div(kblocks, p.kb_per_split);  // no empty split
-    }
+    if (int4) s = s < kblocks / kMinKbPerSplit ? s : kblocks / kMinKbPerSplit;
+    else
+      while (s > 1 && kblocks < s * ((tiles * s <= cus) ? 16 : 24)) --s;
+  } else if (!int4 && (p.cfg == kV3M128N128 || p.cfg == kV3M128N128S3) && kblocks >= 192 &&
+             tiles <= 3LL * cus) {
+    // Long K (>= 12288) at one tile per CU, or 1.25..1.75 / 2.25..2.75 per
+    // CU: two K splits even out the CUs' share (and give one-per-CU launches
+    // two waves per SIMD): 1024 x 4096 x 12288 97 us instead of 105 us,
+    // 1024 / 2048 x 5120 x 25600 262 / 445 us instead of 290 / 497 us.
+    const int64_t q4 = (tiles % cus) * 4;  // fractional tiles per CU, x 4 CUs
+    if (tiles == cus || (q4 >= cus && q4 <= 3 * cus)) s = 2;
+  }
+  if (s >= 2) {
+    p.kb_per_split = (int)ceil_div(kblocks, s);
+    p.splits = (int)ceil_div(kblocks, p.kb_per_split);  // no empty split
   }
   // 128x128 tiles that leave one to two workgroups (two wavefronts per SIMD)
   // on a CU: the interleaved schedule (+8..16% on 384 and 512 tiles of

@@ -422,23 +422,27 @@ def test_gemv_every_planner_rule(m, n, k):
 
 
 # One shape per rule of the GEMM planner (w8a16_gemm.hip plan_gemm), with a
-# 256-CU MI355X: tiles = ceil(M/BM) * ceil(N/BN); a K split when tiles are
-# fewer than CUs x workgroups/CU and K has >= 2 x 16 blocks of 64.
+# 256-CU MI355X: tiles = ceil(M/BM) * ceil(N/BN); a K split below one tile per
+# CU (>= 16 or 24 blocks of 64 per split), or for K >= 12288 at one tile per CU
+# or a CU share of 1.25..1.75 / 2.25..2.75 tiles.
 GEMM_POLICY = [
     (100, 520, 1032),    # M < 128: 64x256 tiles
-    (1024, 8200, 264),   # M >= 1024, N >= 8192: 128x256 tiles, 2 workgroups/CU
+    (1024, 8200, 264),   # M >= 1024, 520 tiles of 128x128 (3 per CU) cost less than 264 of 128x256
+    (1024, 24576, 136),  # M >= 1024, 768 tiles of 128x256 tie with 1536 of 128x128: 128x256; K tail
     (1100, 1000, 520),   # M >= 1024, N < 8192: 128x128 tiles, 3 workgroups/CU
     (1300, 3900, 1032),  # the same with 341 tiles (1..2 per CU): interleaved schedule, ragged M/N/K
     (1024, 16384, 128),  # M >= 1024, 256x256 tiles fill whole rounds (4 x 64 = 256)
     (1025, 65300, 72),   # the same rule on ragged M, N, K (5 x 256 = 1280 tiles)
-    (200, 16400, 136),   # 128 <= M < 1024, N >= 16384: 128x256 tiles
+    (200, 16400, 136),   # 128 <= M < 1024: 258 tiles of 128x128 (1..2 per CU): interleaved schedule
+    (500, 25600, 136),   # 128 <= M < 1024: 400 tiles of 128x256 tie with 800 of 128x128: 128x256
     (300, 384, 1024),    # 128 <= M < 1024, N < 16384: 128x128 tiles, 3 stages
     (300, 384, 4096),    # 9 tiles, 64 K blocks: 4-way K split of 16 blocks
-    (512, 4096, 1032),   # 128 <= M < 1024: 256 tiles (one per CU), no K split; K tail
+    (512, 4096, 1032),   # 128 <= M < 1024: 128 tiles, 17 K blocks: too short to split; K tail
     (640, 7000, 520),    # 128 <= M < 1024: 275 tiles (1..2 per CU), interleaved schedule
     (200, 1000, 2056),   # 16 tiles, 33 K blocks: 2-way split, K tail in split 1
     (100, 520, 4096),    # M < 128: 6 tiles, 4-way K split
-    (1024, 2048, 8192),  # M >= 1024: 128 tiles of 128x128, 6-way K split
+    (1024, 2048, 8192),  # M >= 1024: 128 tiles of 128x128, 5-way K split (>= 24 blocks each)
+    (1024, 4096, 12288), # 256 tiles (one per CU), K >= 12288: 2-way K split
     # M <= 64: 32x64 / 64x64 tiles, split to ~3 workgroups per CU
     (20, 4096, 4096),    # M 17..32: 64 tiles, 8-way split (8 K blocks each)
     (48, 5120, 8192),    # M 33..64: 80 tiles, 8-way split
