@@ -779,7 +779,7 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     // 4096 (and 1..2% inside the MLP step), where one weight matrix of the
     // same shape runs 2..9% faster with 256x256.
     p.cfg = kV3M256N256;
-  } else if (!int4 && t128 <= 6LL * cus) {
+  } else if (t128 <= 6LL * cus) {
     // Up to six 128x128 tiles per CU the tiles a CU gets decide the time:
     // a launch takes ceil(tiles / CUs) tile times, a 128x256 tile costing
     // two 128x128 ones.  The cheaper shape wins; on a tie 128x128 when it
@@ -812,10 +812,8 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     // 26.5 us with 2 splits, 28.6 us with 4).
     s = (int)(slots / tiles);
     s = s < kMaxGemmSplits ? s : kMaxGemmSplits;
-    if (int4) s = s < kblocks / kMinKbPerSplit ? s : kblocks / kMinKbPerSplit;
-    else
-      while (s > 1 && kblocks < s * ((tiles * s <= cus) ? 16 : 24)) --s;
-  } else if (!int4 && (p.cfg == kV3M128N128 || p.cfg == kV3M128N128S3) && kblocks >= 192 &&
+    while (s > 1 && kblocks < s * ((tiles * s <= cus) ? 16 : 24)) --s;
+  } else if ((p.cfg == kV3M128N128 || p.cfg == kV3M128N128S3) && kblocks >= 192 &&
              tiles <= 3LL * cus) {
     // Long K (>= 12288) at one tile per CU, or 1.25..1.75 / 2.25..2.75 per
     // CU: two K splits even out the CUs' share (and give one-per-CU launches
