@@ -14,6 +14,10 @@
 //     verbatim and each lane's 16 bytes are exactly its two MFMA B operands,
 //     dequantized in registers right before the MFMAs (exact, v_perm +
 //     v_pk_add);
+//   * in a 1 x N wavefront grid no two wavefronts read the same B strip, so
+//     the 128x256 and 128x128 (3 per CU) tiles skip LDS for B: each wavefront
+//     loads its strips one K block ahead straight into VGPRs (BR), which
+//     halves the LDS writes of a 128x256 tile and cuts its LDS reads by 20%;
 //   * tiles are ordered so that the workgroups one XCD runs at the same time
 //     (the hardware deals workgroup ids round-robin over the 8 XCDs) cover a
 //     compact block of output tiles and share A and B rows in their L2;
@@ -25,6 +29,8 @@
 //     the workspace and the last split to arrive sums all partials in split
 //     order (deterministic) before the epilogue;
 //   * the per-channel scale and bias are applied in the fp32 epilogue.
+#include <type_traits>
+
 #include "w8a16_common.h"
 #include "w8a16_internal.h"
 
@@ -207,7 +213,7 @@ __device__ __forceinline__ void store_tile(const TileTarget& t, const floatx4 (&
 // raised issue priority (s_setprio 1).  Same arithmetic in the same order;
 // chosen where two wavefronts per SIMD are resident (see plan_gemm).
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8,
-          bool IL = false>
+          bool IL = false, bool BR = false>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(OCC * WAVES_M * WAVES_N / 4, 8)))
 void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
@@ -220,14 +226,19 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   constexpr bool GS = WF == kWfInt4Grp;
   constexpr int S_BYTES = GS ? 1024 : 0;  // one wavefront DMA of scale rows
   static_assert(!GS || 2 * BN * 2 <= S_BYTES, "two scale rows of BN fp16 fit one DMA");
-  constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+  // BR: each wavefront loads its own B strips straight into registers (in a
+  // 1 x N grid no two wavefronts share a strip, so staging B in LDS only adds
+  // a DMA write and a read per byte); LDS then holds A (and scales) only.
+  constexpr int S_OFF = A_BYTES + (BR ? 0 : B_BYTES);
+  constexpr int STAGE = S_OFF + S_BYTES;
   constexpr int A_LOADS = A_BYTES / (NT * 16);
-  constexpr int B_LOADS = B_BYTES / (NT * 16);
+  constexpr int B_LOADS = BR ? 0 : B_BYTES / (NT * 16);
   constexpr int LOADS = A_LOADS + B_LOADS;
-  static_assert(A_LOADS >= 1 && B_LOADS >= 1 && A_LOADS * NT * 16 == A_BYTES &&
-                    B_LOADS * NT * 16 == B_BYTES,
+  static_assert(A_LOADS >= 1 && (BR || B_LOADS >= 1) && A_LOADS * NT * 16 == A_BYTES &&
+                    (BR || B_LOADS * NT * 16 == B_BYTES),
                 "tile does not split into whole 1 KB wavefront loads");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
+  static_assert(!BR || (STAGES == 2 && WAVES_M == 1 && !IL), "register B: 2 stages, 1 x N grid");
 
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
 
@@ -260,7 +271,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     arow_off[i] = (uint32_t)((int64_t)r * a.ldx * 2);
     aoff[i] = arow_off[i] + acol[i] * 2;
   }
-  uint32_t boff[B_LOADS];
+  uint32_t boff[B_LOADS > 0 ? B_LOADS : 1];
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
     if (WF) {
@@ -312,8 +323,9 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
                                     : (int64_t)kb * kTileBytes);
 #pragma unroll
     for (int l = 0; l < B_LOADS; ++l) dma16s(boff[l], bb, st + A_BYTES + (wave_u * B_LOADS + l) * 1024);
+    (void)bb;
     if (GS && wave_u == 0)
-      dma16s(soff, sbase + (int64_t)((2 * kb) >> a.gshift) * tt.N, st + A_BYTES + B_BYTES);
+      dma16s(soff, sbase + (int64_t)((2 * kb) >> a.gshift) * tt.N, st + S_OFF);
   };
   auto fix_tail = [&](int i) {
     const int kb = kb0 + i;
@@ -339,6 +351,75 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   // group-wise: this lane's scale row in the block (gs = 32: positions 16g..16g+15
   // lie in group g/2 of the block's two)
   const int s4off = GS ? (((a.gshift == 0) ? (lane >> 5) : 0) * BN + wn * TN * 16 + (lane & 15)) * 2 : 0;
+  // Register B: this lane's byte offset in each of the wavefront's strips.
+  uint32_t broff[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int t = min(strip0 + wn * TN + j, tt.nstrips - 1) - strip0;
+    broff[j] = (uint32_t)t * (uint32_t)a.wtiles * kTileBytes + (WF ? (uint32_t)b4off : (uint32_t)lane * 16);
+  }
+  using BRaw = typename std::conditional<WF != kWfInt8, uint2, uint4>::type;
+  BRaw breg[TN];
+  const __amdgpu_buffer_rsrc_t brsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(bbase), (short)0, -1, 0x00020000);
+  // Issued right after the A DMA; the memory clobber keeps the compiler from
+  // sinking them behind the MFMAs of the current block.
+  auto load_b = [&](int i) {
+    const int kb = kb0 + i;
+    const uint32_t boffk = WF ? (uint32_t)(kb >> 1) * kTileBytes + (kb & 1) * (kTileBytes / 2)
+                              : (uint32_t)kb * kTileBytes;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (WF == kWfInt8) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(brsrc, broff[j], boffk, 0);
+        breg[j] = *reinterpret_cast<const BRaw*>(&v);
+      } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(brsrc, broff[j], boffk, 0);
+        breg[j] = *reinterpret_cast<const BRaw*>(&v);
+      }
+    }
+    __asm__ volatile("" ::: "memory");
+  };
+  // Dequantize the registers of block i; the empty asm pins the results
+  // before the next block's loads are issued, so the compiler's own wait for
+  // these loads is a vmcnt(0) that the loop's wait has already satisfied.
+  auto dequant_b = [&](int i, half8 (&bq)[2][TN]) {
+    const uint8_t* st = smem + (i % STAGES) * STAGE;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (WF == kWfInt8) {
+        const uint4 d = *reinterpret_cast<const uint4*>(&breg[j]);
+        bq[0][j] = dequant8(d.x, d.y);
+        bq[1][j] = dequant8(d.z, d.w);
+      } else {
+        const uint2 d = *reinterpret_cast<const uint2*>(&breg[j]);
+        if constexpr (GS) {
+          const _Float16 sc = *reinterpret_cast<const _Float16*>(st + S_OFF + s4off + j * 32);
+          bq[0][j] = dequant8_i4_scaled(d.x, sc);
+          bq[1][j] = dequant8_i4_scaled(d.y, sc);
+        } else {
+          bq[0][j] = dequant8_i4(d.x);
+          bq[1][j] = dequant8_i4(d.y);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) __asm__ volatile("" ::"v"(bq[0][j]), "v"(bq[1][j]));
+  };
+  auto compute_br = [&](int i, const half8 (&bq)[2][TN]) {
+    const uint8_t* st = smem + (i % STAGES) * STAGE;
+#pragma unroll
+    for (int step = 0; step < 2; ++step) {
+      half8 af[TM];
+      const int ao = step == 0 ? aoff0 : aoff1;
+#pragma unroll
+      for (int r = 0; r < TM; ++r) af[r] = *reinterpret_cast<const half8*>(st + ao + r * 16 * 128);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(af[r], bq[step][j], acc[r][j]);
+    }
+  };
   auto compute = [&](int i) {
     const uint8_t* st = smem + (i % STAGES) * STAGE;
     if constexpr (WF != kWfInt8) {
@@ -347,7 +428,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         braw[j] = *reinterpret_cast<const uint2*>(st + A_BYTES + (wn * TN + j) * B_STRIP + b4off);
-        if (GS) sc[GS ? j : 0] = *reinterpret_cast<const _Float16*>(st + A_BYTES + B_BYTES + s4off + j * 32);
+        if (GS) sc[GS ? j : 0] = *reinterpret_cast<const _Float16*>(st + S_OFF + s4off + j * 32);
       }
 #pragma unroll
       for (int step = 0; step < 2; ++step) {
@@ -413,6 +494,34 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     }
   };
 
+  if constexpr (BR) {
+    // Two stages: A(i+1) by DMA and B(i+1) into registers are in flight
+    // during compute(i); every wait is a full vmcnt(0).
+    issue(0, true);
+    load_b(0);
+    int i = 0;
+    for (; i < nk - 2; ++i) {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      barrier_lds();
+      half8 bq[2][TN];
+      dequant_b(i, bq);
+      issue(i + 1, false);
+      load_b(i + 1);
+      compute_br(i, bq);
+    }
+    for (; i < nk; ++i) {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (k_tail && kb0 + i == a.kblocks - 1) fix_tail(i);
+      barrier_lds();
+      half8 bq[2][TN];
+      dequant_b(i, bq);
+      if (i + 1 < nk) {
+        issue(i + 1, true);
+        load_b(i + 1);
+      }
+      compute_br(i, bq);
+    }
+  } else {
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < nk) issue(s, true);
@@ -455,6 +564,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     // Everyone is past compute(i-1): its stage can be refilled.
     if (i + STAGES - 1 < nk) issue(i + STAGES - 1, true);
     compute(i);
+  }
   }
 
   if (a.splits > 1) {
@@ -645,14 +755,14 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8,
-          bool IL = false>
+          bool IL = false, bool BR = false>
 hipError_t launch_v3_t(const GemmKernelArgs& ka, hipStream_t stream) {
   static_assert(!IL || WF == kWfInt8, "the interleaved schedule is an int8 variant");
   const int64_t tiles = (int64_t)ka.tiles_m * ka.tiles_n;
   if (tiles <= 0 || tiles > 0x7fffffff || ka.splits < 1 || ka.splits > 65535 ||
       !v3_offsets_fit(ka, BM, BN))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, WF, IL>),
+  hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, WF, IL, BR>),
                      dim3((unsigned)tiles, (unsigned)ka.splits), dim3(WAVES_M * WAVES_N * 64), 0,
                      stream, ka);
   return hipGetLastError();
@@ -671,8 +781,8 @@ hipError_t launch_dma_t(const GemmKernelArgs& ka, hipStream_t stream) {
 
 // Tile configurations (measured on MI355X over the BASELINE prefill shapes).
 enum GemmCfgId {
-  kV3M128N256,    // 4 wavefronts 1x4, 2 stages, 2 workgroups/CU: wide N
-  kV3M128N128,    // 4 wavefronts 1x4, 2 stages, 3 workgroups/CU: M >= 1024, N < 8192
+  kV3M128N256,    // 4 wavefronts 1x4, 2 stages, 2 workgroups/CU, B in registers: wide N
+  kV3M128N128,    // 4 wavefronts 1x4, 2 stages, 3 workgroups/CU, B in registers: M >= 1024, N < 8192
   kV3M128N128S3,  // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: moderate M and N
   kV3M64N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: small M
   kV3M256N256,    // 8 wavefronts 2x4, 2 stages, 1 workgroup/CU: whole rounds of big tiles
@@ -693,8 +803,8 @@ namespace {
 template <int WF>
 hipError_t launch_gemm4(int cfg, const GemmKernelArgs& ka, hipStream_t stream) {
   switch (cfg) {
-    case kV3M128N256: return launch_v3_t<128, 256, 1, 4, 2, 2, WF>(ka, stream);
-    case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3, WF>(ka, stream);
+    case kV3M128N256: return launch_v3_t<128, 256, 1, 4, 2, 2, WF, false, true>(ka, stream);
+    case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3, WF, false, true>(ka, stream);
     case kV3M128N128S3: return launch_v3_t<128, 128, 1, 4, 3, 2, WF>(ka, stream);
     case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2, WF>(ka, stream);
     case kV3M256N256: return launch_v3_t<256, 256, 2, 4, 2, 1, WF>(ka, stream);
@@ -909,8 +1019,8 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
   if (pr.wf == kWfInt4) return launch_gemm4<kWfInt4>(p.cfg, ka, stream);
   if (pr.wf == kWfInt4Grp) return launch_gemm4<kWfInt4Grp>(p.cfg, ka, stream);
   switch (p.cfg) {
-    case kV3M128N256: return launch_v3_t<128, 256, 1, 4, 2, 2>(ka, stream);
-    case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3>(ka, stream);
+    case kV3M128N256: return launch_v3_t<128, 256, 1, 4, 2, 2, kWfInt8, false, true>(ka, stream);
+    case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3, kWfInt8, false, true>(ka, stream);
     case kV3M128N128S3: return launch_v3_t<128, 128, 1, 4, 3, 2>(ka, stream);
     case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2>(ka, stream);
     case kV3M256N256: return launch_v3_t<256, 256, 2, 4, 2, 1>(ka, stream);

@@ -93,6 +93,8 @@ CASES = [
     (1024, 4096, 4096, 32), (1100, 1008, 640, 128), (300, 1024, 8192, 32), (256, 512, 4096, 0),
     # int4-only GEMV rules: M 3..4 many strips with x in LDS; M 5..16 long K, 2-way split
     (4, 12288, 4096, 32), (3, 10240, 1088, 0), (16, 4096, 12288, 32), (8, 2048, 8192, 128),
+    # GEMM tiles with B loaded into registers: 128x256 (ragged M; per-channel), 128x128
+    (520, 25600, 1024, 32), (2048, 12288, 1024, 0), (1024, 12288, 2048, 128),
 ]
 
 
