@@ -896,10 +896,20 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     // lands one to two tiles per CU (the interleaved schedule below), else
     // 128x256.  (Measured over the Qwen3-8B and Qwen3-VL-32B projections at
     // M 128..4096 on MI355X: e.g. fused q/k/v 10240 x 5120 at M 1024 / 2048
-    // 100.6 / 171 us instead of 110.5 / 187 us with 128x256, gate/up
-    // 24576 x 4096 at M 512 93.9 instead of 99.7 us.)
+    // 100.6 / 171 us instead of 110.5 / 187 us with 128x256.)  Exception:
+    // at two to three 128x128 tiles per CU and at least 1.5 128x256 tiles
+    // per CU, both shapes finish in one round and the 128x256 tile, with its
+    // B strips in registers, does more work per cycle; so there 128x256 wins
+    // unless K is long enough for the K split below (gate/up 24576 x 4096 at
+    // M 512: 92.8 instead of 95.1 us; fused q/k/v 6144 x 4096 at M 2048: 83.5
+    // instead of 86.9 us; 12288 x 4096 at M 1024: 83.0 instead of 86.8 us).
+    // With fewer 128x256 tiles the CUs holding two of them decide, and the
+    // results scatter (-6..+8%), so the rule stays as it was.
     const int64_t r256 = ceil_div(t128x256, cus) * 2, r128 = ceil_div(t128, cus);
-    const bool use128 = r128 < r256 || (r128 == r256 && t128 > cus && t128 <= 2LL * cus);
+    const bool one_round = t128 > 2LL * cus && t128 <= 3LL * cus && 2 * t128x256 >= 3LL * cus &&
+                           ceil_div(K, 64) < 192;
+    const bool use128 =
+        !one_round && (r128 < r256 || (r128 == r256 && t128 > cus && t128 <= 2LL * cus));
     p.cfg = !use128 ? kV3M128N256
                     : (M < 1024 && t128 <= 2LL * cus) ? kV3M128N128S3 : kV3M128N128;
   } else if (M >= 1024) {

@@ -428,6 +428,7 @@ def test_gemv_every_planner_rule(m, n, k):
 GEMM_POLICY = [
     (100, 520, 1032),    # M < 128: 64x256 tiles
     (1024, 8200, 264),   # M >= 1024, 520 tiles of 128x128 (3 per CU) cost less than 264 of 128x256
+    (1024, 12288, 200),  # 768 tiles of 128x128 (3 per CU): one round of 384 128x256 tiles; K tail
     (1024, 24576, 136),  # M >= 1024, 768 tiles of 128x256 tie with 1536 of 128x128: 128x256; K tail
     (1100, 1000, 520),   # M >= 1024, N < 8192: 128x128 tiles, 3 workgroups/CU
     (1300, 3900, 1032),  # the same with 341 tiles (1..2 per CU): interleaved schedule, ragged M/N/K
