@@ -706,7 +706,7 @@ hipError_t launch_gemv_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStrea
 // Int4 launches take the same rules with K counted in 128-wide tiles (one
 // 1 KB tile per 128 positions, as an int8 tile holds 64): a configuration
 // runs with half its unroll (its int4 tiles carry twice the activation
-// registers), and activations always come from global memory.
+// registers), except one per-channel XL instance below.
 template <int WF>
 hipError_t launch_gemv4_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStream_t stream) {
   // x staged in LDS where the planner asks for it and int4's 256 bytes of x
@@ -715,8 +715,16 @@ hipError_t launch_gemv4_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStre
     return gemv_lds_bytes(1, ns, w, true, ka.M, ka.kb_per_split, kTileK4) <= 65536;
   };
   switch (p.cfg) {
+    // With x in LDS no activation registers ride the pipeline, so the
+    // 16-wavefront per-channel instance keeps the int8 unroll (down 4096 x
+    // 12288 at M 1: 7.36..7.70 instead of 7.78..8.33 us).  At the int8
+    // unroll the group-wise instances lose 10..13% to their scale loads and
+    // the 8-wavefront one 1..2%, so they keep half.
     case kG1x1W16U4XL:
-      if (xl_fits(1, 16)) return launch_t<1, 1, 16, 1, true, true, WF>(ka, p, stream);
+      if (xl_fits(1, 16)) {
+        if (WF == kWfInt4) return launch_t<1, 1, 16, 2, true, true, WF>(ka, p, stream);
+        return launch_t<1, 1, 16, 1, true, true, WF>(ka, p, stream);
+      }
       return launch_t<1, 1, 16, 1, false, true, WF>(ka, p, stream);
     case kG1x1W8U4XL:
       if (xl_fits(1, 8)) return launch_t<1, 1, 8, 2, true, true, WF>(ka, p, stream);
