@@ -422,7 +422,40 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   };
   auto compute = [&](int i) {
     const uint8_t* st = smem + (i % STAGES) * STAGE;
-    if constexpr (WF != kWfInt8) {
+    if constexpr (WF != kWfInt8 && IL) {
+      // The int8 interleaved schedule below with int4 B (and group-wise
+      // scale reads among the first LDS reads).
+      __builtin_amdgcn_s_setprio(1);
+      uint2 braw[TN];
+      _Float16 sc[GS ? TN : 1];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        braw[j] = *reinterpret_cast<const uint2*>(st + A_BYTES + (wn * TN + j) * B_STRIP + b4off);
+        if (GS) sc[GS ? j : 0] = *reinterpret_cast<const _Float16*>(st + S_OFF + s4off + j * 32);
+      }
+      half8 af0[TM], af1[TM];
+#pragma unroll
+      for (int r = 0; r < TM; ++r) af0[r] = *reinterpret_cast<const half8*>(st + aoff0 + r * 16 * 128);
+#pragma unroll
+      for (int r = 0; r < TM; ++r) af1[r] = *reinterpret_cast<const half8*>(st + aoff1 + r * 16 * 128);
+#pragma unroll
+      for (int step = 0; step < 2; ++step)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const uint32_t d = step == 0 ? braw[j].x : braw[j].y;
+          const half8 b = GS ? dequant8_i4_scaled(d, sc[GS ? j : 0]) : dequant8_i4(d);
+#pragma unroll
+          for (int r = 0; r < TM; ++r) acc[r][j] = mfma16x16x32(step == 0 ? af0[r] : af1[r], b, acc[r][j]);
+        }
+      __builtin_amdgcn_sched_group_barrier(0x100, (GS ? 2 : 1) * TN + TM, 0);
+#pragma unroll
+      for (int r = 0; r < TM; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * TM * TN - TM, 0);
+      __builtin_amdgcn_s_setprio(0);
+    } else if constexpr (WF != kWfInt8) {
       uint2 braw[TN];
       _Float16 sc[GS ? TN : 1];
 #pragma unroll
@@ -757,7 +790,6 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8,
           bool IL = false, bool BR = false>
 hipError_t launch_v3_t(const GemmKernelArgs& ka, hipStream_t stream) {
-  static_assert(!IL || WF == kWfInt8, "the interleaved schedule is an int8 variant");
   const int64_t tiles = (int64_t)ka.tiles_m * ka.tiles_n;
   if (tiles <= 0 || tiles > 0x7fffffff || ka.splits < 1 || ka.splits > 65535 ||
       !v3_offsets_fit(ka, BM, BN))
@@ -789,7 +821,7 @@ enum GemmCfgId {
   kDmaM128N128,   // 64-bit addresses: when the v3 32-bit offsets could overflow
   kV3M32N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 17..32, with K splits
   kV3M64N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 33..64, with K splits
-  kV3M128N128IL,  // kV3M128N128 with the interleaved MFMA schedule (int8): 1..2 tiles per CU
+  kV3M128N128IL,  // kV3M128N128 with the interleaved MFMA schedule: 1..2 tiles per CU
   kGemmCfgCount
 };
 
@@ -808,6 +840,14 @@ hipError_t launch_gemm4(int cfg, const GemmKernelArgs& ka, hipStream_t stream) {
     case kV3M128N128S3: return launch_v3_t<128, 128, 1, 4, 3, 2, WF>(ka, stream);
     case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2, WF>(ka, stream);
     case kV3M256N256: return launch_v3_t<256, 256, 2, 4, 2, 1, WF>(ka, stream);
+    case kV3M128N128IL:
+      // Group-wise at M >= 1024 (where the plan replaced the 128x128 tile
+      // with B in registers): that tile is 4% faster than the interleaved
+      // schedule (its scale reads sit in the LDS read groups); below M 1024
+      // the interleaved schedule replaces the 3-stage tile, +14%.
+      if (WF == kWfInt4Grp && ka.M >= 1024)
+        return launch_v3_t<128, 128, 1, 4, 2, 3, WF, false, true>(ka, stream);
+      return launch_v3_t<128, 128, 1, 4, 2, 3, WF, true>(ka, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -950,8 +990,9 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   // on a CU: the interleaved schedule (+8..16% on 384 and 512 tiles of
   // M 1024..4096, K 4096..12288, and +20% on the fused Qwen3-VL-32B q/k/v at
   // M = 512; -1..3% at one tile per CU or 2.5..3 per CU, where the plain
-  // schedule stays).
-  if (!int4 && (p.cfg == kV3M128N128 || p.cfg == kV3M128N128S3) && p.splits == 1 && tiles > cus &&
+  // schedule stays).  Int4 alike: per-channel +6..32% (Qwen3-8B / VL-32B
+  // q/k/v and o at M 512..2048), group-wise +14% below M 1024.
+  if ((p.cfg == kV3M128N128 || p.cfg == kV3M128N128S3) && p.splits == 1 && tiles > cus &&
       tiles <= 2LL * cus)
     p.cfg = kV3M128N128IL;
   return p;

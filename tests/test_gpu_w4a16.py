@@ -95,6 +95,8 @@ CASES = [
     (4, 12288, 4096, 32), (3, 10240, 1088, 0), (16, 4096, 12288, 32), (8, 2048, 8192, 128),
     # GEMM tiles with B loaded into registers: 128x256 (ragged M; per-channel), 128x128
     (520, 25600, 1024, 32), (2048, 12288, 1024, 0), (1024, 12288, 2048, 128),
+    # GEMM interleaved schedule (one to two 128x128 tiles per CU), group-wise
+    (520, 8192, 1024, 32), (1024, 6144, 1024, 128),
 ]
 
 
