@@ -985,6 +985,17 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   if (s >= 2) {
     p.kb_per_split = (int)ceil_div(kblocks, s);
     p.splits = (int)ceil_div(kblocks, p.kb_per_split);  // no empty split
+    // A split count sized for the 3-stage tile (two workgroups per CU) that
+    // leaves more than one workgroup per CU runs faster on the 2-stage tile
+    // with B in registers, except for int8 at long K, where the third stage
+    // hides more of the weights' HBM latency.  (Four rotated weight copies:
+    // Qwen3-VL-32B o at M 512, 160 tiles in three splits, 46.5 instead of
+    // 51.1 us; 12288 x 4096 at M 256 and 4096 x 4096 at M 768 +6%; int4
+    // +4..8.5% including K 12288..25600; int8 4096 x 12288 at M 512 -3.8%.)
+    // The split count stays the 3-stage tile's: sized for three workgroups
+    // per CU it would be four, 131 instead of 118 us on VL down.
+    if (p.cfg == kV3M128N128S3 && tiles * p.splits > cus && (int4 || kblocks < 192))
+      p.cfg = kV3M128N128;
   }
   // 128x128 tiles that leave one to two workgroups (two wavefronts per SIMD)
   // on a CU: the interleaved schedule (+8..16% on 384 and 512 tiles of

@@ -443,6 +443,7 @@ GEMM_POLICY = [
     (200, 1000, 2056),   # 16 tiles, 33 K blocks: 2-way split, K tail in split 1
     (100, 520, 4096),    # M < 128: 6 tiles, 4-way K split
     (1024, 2048, 8192),  # M >= 1024: 128 tiles of 128x128, 5-way K split (>= 24 blocks each)
+    (500, 5000, 8200),   # 160 tiles, 3-way split (two per CU): 128x128 with B in registers; K tail
     (1024, 4096, 12288), # 256 tiles (one per CU), K >= 12288: 2-way K split
     # M <= 64: 32x64 / 64x64 tiles, split to ~3 workgroups per CU
     (20, 4096, 4096),    # M 17..32: 64 tiles, 8-way split (8 K blocks each)
