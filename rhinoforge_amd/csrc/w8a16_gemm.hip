@@ -817,7 +817,7 @@ enum GemmCfgId {
   kV3M128N128,    // 4 wavefronts 1x4, 2 stages, 3 workgroups/CU, B in registers: M >= 1024, N < 8192
   kV3M128N128S3,  // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: moderate M and N
   kV3M64N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: small M
-  kV3M256N256,    // 8 wavefronts 2x4, 2 stages, 1 workgroup/CU: whole rounds of big tiles
+  kV3M256N256,    // (unused: 128x256 with B in registers is faster on every shape measured)
   kDmaM128N128,   // 64-bit addresses: when the v3 32-bit offsets could overflow
   kV3M32N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 17..32, with K splits
   kV3M64N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 33..64, with K splits
@@ -839,7 +839,6 @@ hipError_t launch_gemm4(int cfg, const GemmKernelArgs& ka, hipStream_t stream) {
     case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3, WF, false, true>(ka, stream);
     case kV3M128N128S3: return launch_v3_t<128, 128, 1, 4, 3, 2, WF>(ka, stream);
     case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2, WF>(ka, stream);
-    case kV3M256N256: return launch_v3_t<256, 256, 2, 4, 2, 1, WF>(ka, stream);
     case kV3M128N128IL:
       // Group-wise at M >= 1024 (where the plan replaced the 128x128 tile
       // with B in registers): that tile is 4% faster than the interleaved
@@ -915,20 +914,11 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     cols256 += ceil_div(Ns[i], 256);
     cols128 += ceil_div(Ns[i], 128);
   }
-  const int64_t t256 = ceil_div(M, 256) * cols256;         // 256x256 tiles
   const int64_t t128x256 = ceil_div(M, 128) * cols256;     // 128x256 tiles
   const int64_t t128 = ceil_div(M, 128) * cols128;         // 128x128 tiles
   GemmPlan p;
   if (M < 128) {
     p.cfg = kV3M64N256;
-  } else if (M >= 1024 && (t256 % cus == 0 || t256 >= 4 * cus) && nproj == 1) {
-    // 256x256 tiles only when they fill whole rounds of the chip (or many
-    // rounds): at 1.5 rounds the half-empty last round costs more than the
-    // bigger tile gains.  A launch of several projections (gate/up) keeps
-    // 128x256: measured 0.5..2% faster on the fused gate/up at M 2048 and
-    // 4096 (and 1..2% inside the MLP step), where one weight matrix of the
-    // same shape runs 2..9% faster with 256x256.
-    p.cfg = kV3M256N256;
   } else if (t128 <= 6LL * cus) {
     // Up to six 128x128 tiles per CU the tiles a CU gets decide the time:
     // a launch takes ceil(tiles / CUs) tile times, a 128x256 tile costing
@@ -953,7 +943,11 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     p.cfg = !use128 ? kV3M128N256
                     : (M < 1024 && t128 <= 2LL * cus) ? kV3M128N128S3 : kV3M128N128;
   } else if (M >= 1024) {
-    p.cfg = ntotal >= 8192 ? kV3M128N256 : kV3M128N128;
+    // Beyond six 128x128 tiles per CU: 128x256 with B in registers, also on
+    // whole rounds of 256x256 tiles and below N 8192 (4096^3 109 us against
+    // 111 us with 256x256; 8192 x 4096 x 4096 206 us against 216 us with
+    // 256x256 and 231 us with 128x128).
+    p.cfg = kV3M128N256;
   } else {
     p.cfg = ntotal >= 16384 ? kV3M128N256 : kV3M128N128S3;
   }
@@ -1085,7 +1079,6 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
     case kV3M128N128: return launch_v3_t<128, 128, 1, 4, 2, 3, kWfInt8, false, true>(ka, stream);
     case kV3M128N128S3: return launch_v3_t<128, 128, 1, 4, 3, 2>(ka, stream);
     case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2>(ka, stream);
-    case kV3M256N256: return launch_v3_t<256, 256, 2, 4, 2, 1>(ka, stream);
     case kDmaM128N128: return launch_dma_t<128, 128, 1, 4, 3>(ka, stream);
     case kV3M32N64: return launch_v3_t<32, 64, 1, 4, 4, 4>(ka, stream);
     case kV3M64N64: return launch_v3_t<64, 64, 1, 4, 4, 4>(ka, stream);

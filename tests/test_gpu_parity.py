@@ -432,7 +432,7 @@ GEMM_POLICY = [
     (1024, 24576, 136),  # M >= 1024, 768 tiles of 128x256 tie with 1536 of 128x128: 128x256; K tail
     (1100, 1000, 520),   # M >= 1024, N < 8192: 128x128 tiles, 3 workgroups/CU
     (1300, 3900, 1032),  # the same with 341 tiles (1..2 per CU): interleaved schedule, ragged M/N/K
-    (1024, 16384, 128),  # M >= 1024, 256x256 tiles fill whole rounds (4 x 64 = 256)
+    (1024, 16384, 128),  # M >= 1024, 8 x 64 = 512 tiles of 128x256 (two whole rounds)
     (1025, 65300, 72),   # the same rule on ragged M, N, K (5 x 256 = 1280 tiles)
     (200, 16400, 136),   # 128 <= M < 1024: 258 tiles of 128x128 (1..2 per CU): interleaved schedule
     (500, 25600, 136),   # 128 <= M < 1024: 400 tiles of 128x256 tie with 800 of 128x128: 128x256
@@ -678,9 +678,8 @@ def test_linear_multi_gemm_one_launch_ragged_split():
 
 def test_linear_multi_gemm_whole_rounds_two_projections():
     """M=1024, gate/up-like pair N = 8200 (ragged) and 7936, K = 520 (K tail):
-    4 x (33 + 31) = 256 tiles of 256x256 would fill one whole round, the case
-    where a single matrix takes 256x256 tiles and a multi-projection launch
-    128x256.  Each output against the oracle and against a single call."""
+    8 x (33 + 31) = 512 tiles of 128x256 fill two whole rounds.  Each output
+    against the oracle and against a single call."""
     m, k = 1024, 520
     ns = [(8200, True), (7936, False)]
     x = o.make_activation(o.derive_seed(26, "x", m, k), m, k)
