@@ -135,7 +135,10 @@ size_t rf_w8a16_workspace_bytes_multi(int64_t M, const int64_t* Ns, int32_t coun
  *              (rpu_linear.cpp:279-283, 796-808)
  *   y        : fp16 [M, ldy], ldy >= N
  *   M >= 1, N >= 1, K >= 8, K % 8 == 0
- *   kernel   : RF_W8A16_KERNEL_AUTO / _GEMV / _GEMM
+ *   kernel   : RF_W8A16_KERNEL_AUTO / _GEMV / _GEMM.  The GEMV addresses a
+ *              16-row span of x with 32-bit offsets: it returns
+ *              RF_W8A16_EKERNEL when (min(M,16) - 1) * ldx * 2 + 256 >= 2^32
+ *              (AUTO then runs the GEMM, which has a 64-bit-address kernel)
  *   workspace: device buffer of >= rf_w8a16_workspace_bytes(M,N,K) bytes,
  *              counters zeroed as described above; calls that share one
  *              workspace must be ordered (same stream).
@@ -168,7 +171,8 @@ int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w
  *              region zeroed as for rf_w8a16_linear.  Two launches: the GEMV
  *              leaves each workgroup's best per-row key in the workspace, a
  *              second kernel reduces them.
- * Other arguments as rf_w8a16_linear.  Returns RF_W8A16_EKERNEL for M > 64.
+ * Other arguments as rf_w8a16_linear.  Returns RF_W8A16_EKERNEL for M > 64
+ * and for row strides the GEMV cannot address (see rf_w8a16_linear).
  * Replaces the decode lm_head GEMM + argmax pair (src/fused/rpu_qwen3_model.h:
  * 3653-3690 writes the logits; src/ops/rpu_argmax.cpp:485-640 reduces them,
  * int32 result, first index among ties). */
@@ -225,7 +229,9 @@ int rf_w4a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K, int64
 size_t rf_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 /* y = x . W^T (+ b) with a TILE16X128_I4 weight.  group_size: 0 (per-channel
  * scale [N]) or 32 / 64 / 128 (scale [K/group_size][N], 16-byte aligned).
- * kernel, workspace and stream as for rf_w8a16_linear. */
+ * kernel, workspace and stream as for rf_w8a16_linear; the int4 GEMM has no
+ * 64-bit-address kernel and returns RF_W8A16_EKERNEL where a tile's rows
+ * (up to 128 rows of ldx halves) span 4 GB or more. */
 int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void* scale,
                     int32_t group_size, const void* bias, void* y, int64_t ldy, int64_t M,
                     int64_t N, int64_t K, int32_t kernel, void* workspace, size_t workspace_bytes,

@@ -175,7 +175,9 @@ const char* rf_w8a16_status_str(int status) {
     case RF_W8A16_EWORKSPACE: return "workspace missing or smaller than rf_w8a16_workspace_bytes()";
     case RF_W8A16_EHIP: return "HIP runtime error";
     case RF_W8A16_EDEVICE: return "current HIP device is not gfx950 (MI355X)";
-    case RF_W8A16_EKERNEL: return "requested kernel cannot run this shape";
+    case RF_W8A16_EKERNEL:
+      return "requested kernel cannot run this shape (GEMV: M > 64, or a row stride ldx whose "
+             "32-bit offsets over 16 rows overflow)";
     default: return "unknown rf_w8a16 status";
   }
 }
@@ -296,9 +298,14 @@ int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w
     int64_t ntotal = 0;
     for (int i = 0; i < count; ++i) ntotal += projs[i].N;
     kernel = auto_kernel(M, ntotal, K);
+    // A row stride too large for the GEMV's 32-bit offsets: the GEMM (with
+    // its 64-bit-address kernel) runs instead.
+    if (kernel == RF_W8A16_KERNEL_GEMV && !rf::gemv_offsets_fit(M, ldx))
+      kernel = RF_W8A16_KERNEL_GEMM;
   }
   if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
-  if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
+  if (kernel == RF_W8A16_KERNEL_GEMV && (M > 64 || !rf::gemv_offsets_fit(M, ldx)))
+    return RF_W8A16_EKERNEL;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   rf::LinearProblem pr;
@@ -449,9 +456,14 @@ int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void
   if (st != RF_W8A16_OK) return st;
   if (!dev.gfx950) return RF_W8A16_EDEVICE;
 
-  if (kernel == RF_W8A16_KERNEL_AUTO) kernel = auto_kernel_int4(M);
+  if (kernel == RF_W8A16_KERNEL_AUTO) {
+    kernel = auto_kernel_int4(M);
+    if (kernel == RF_W8A16_KERNEL_GEMV && !rf::gemv_offsets_fit(M, ldx))
+      kernel = RF_W8A16_KERNEL_GEMM;
+  }
   if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
-  if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
+  if (kernel == RF_W8A16_KERNEL_GEMV && (M > 64 || !rf::gemv_offsets_fit(M, ldx)))
+    return RF_W8A16_EKERNEL;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   rf::LinearProblem pr;
@@ -482,6 +494,8 @@ int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void
     e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);
   } else {
     const rf::GemmPlan p = rf::plan_gemm(pr.M, &n32, 1, pr.K, dev, true);
+    // The int4 GEMM has no 64-bit-address kernel.
+    if (!rf::gemm_offsets_fit(p, ldx, pr.K, true)) return RF_W8A16_EKERNEL;
     if (p.splits > 1 && !workspace_ok(rf::gemm_workspace_bytes(p))) return RF_W8A16_EWORKSPACE;
     e = rf::launch_gemm(pr, p, p.splits > 1 ? workspace : nullptr, s);
   }
@@ -514,7 +528,7 @@ int rf_w8a16_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int
       !aligned(scale, 2) || (bias && !aligned(bias, 2)) || (y && !aligned(y, 2)) ||
       !aligned(index, 4))
     return RF_W8A16_EALIGN;
-  if (M > 64) return RF_W8A16_EKERNEL;
+  if (M > 64 || !rf::gemv_offsets_fit(M, ldx)) return RF_W8A16_EKERNEL;
   rf::DeviceInfo dev;
   int st = rf::device_info(&dev);
   if (st != RF_W8A16_OK) return st;

@@ -1003,6 +1003,14 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   return p;
 }
 
+bool gemm_offsets_fit(const GemmPlan& p, int64_t ldx, int K, bool int4) {
+  GemmKernelArgs ka;
+  ka.ldx = ldx;
+  ka.kblocks = (int)ceil_div(K, 64);
+  ka.wtiles = int4 ? (int)ceil_div(K, kTileK4) : ka.kblocks;
+  return v3_offsets_fit(ka, p.bm, p.bn);
+}
+
 size_t gemm_workspace_bytes(const GemmPlan& p) {
   if (p.splits <= 1) return 0;
   return (size_t)p.splits * (size_t)p.tiles_m * (size_t)p.tiles_n * (size_t)p.bm * (size_t)p.bn *

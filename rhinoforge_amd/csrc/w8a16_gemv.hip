@@ -103,22 +103,26 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 
 // Activation fragment of one tile for every m-tile read from global memory:
 // x[m][k .. k+15] with m = 16*mt + lane%16, k = 64*kb + 16*(lane/16).
-// Addresses are a wave-uniform base (x + 64*kb, scalar) plus a per-lane
-// 32-bit offset fixed for the whole call (xoff[mt]: row m, lane group), so a
-// load costs no vector address math.  Rows m >= M read row M-1 instead (their
-// MFMA output rows are never stored).  KT (K % 64 != 0, a launch-time
+// Addresses are a wave-uniform 64-bit base per m-tile (xrow[mt] = first row
+// of the m-tile, plus 64*kb: scalar) and a per-lane 32-bit offset fixed for
+// the whole call (xoff[mt]: row within the m-tile, lane group), so a load
+// costs no vector address math.  The 32-bit part spans at most 15 rows; the
+// host checks that it cannot overflow (gemv_offsets_fit).  Rows m >= M read
+// row M-1 instead (their MFMA output rows are never stored).  KT (K % 64 != 0, a launch-time
 // choice) clamps every chunk into the row and zeroes the chunks past K with
 // selects; without it the load path has no branch or select at all, which
 // keeps the compiler's load-wait bookkeeping exact (a branch around a load
 // makes it fall back to waiting for every load in flight).
 // K % 8 == 0, so a chunk that starts below K ends below K.
 template <int MT, bool KT>
-__device__ __forceinline__ void load_x_global(const GemvKernelArgs& a, int kb, const uint32_t (&xoff)[MT],
-                                              int lane, half8 (&xa)[MT][2]) {
-  const uint8_t* xb = reinterpret_cast<const uint8_t*>(a.x) + (int64_t)kb * (kTileK * 2);
+__device__ __forceinline__ void load_x_global(const GemvKernelArgs& a, int kb,
+                                              const uint8_t* const (&xrow)[MT],
+                                              const uint32_t (&xoff)[MT], int lane,
+                                              half8 (&xa)[MT][2]) {
   if (!KT) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      const uint8_t* xb = xrow[mt] + (int64_t)kb * (kTileK * 2);
       xa[mt][0] = as_half8(load_u4(xb + xoff[mt]));
       xa[mt][1] = as_half8(load_u4(xb + xoff[mt] + 16));
     }
@@ -128,6 +132,7 @@ __device__ __forceinline__ void load_x_global(const GemvKernelArgs& a, int kb, c
     const int d0 = (min(k, a.K - 8) - k) * 2, d1 = (min(k + 8, a.K - 8) - (k + 8)) * 2;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      const uint8_t* xb = xrow[mt] + (int64_t)kb * (kTileK * 2);
       const half8 v0 = as_half8(load_u4(xb + xoff[mt] + d0));
       const half8 v1 = as_half8(load_u4(xb + xoff[mt] + 16 + d1));
       xa[mt][0] = k < a.K ? v0 : half8{};
@@ -142,18 +147,21 @@ __device__ __forceinline__ void load_x_global(const GemvKernelArgs& a, int kb, c
 // for int4, so with KT (K % 128 == 64) a lane's 32 positions are either all
 // below K or all past it; the latter read a clamped chunk and are zeroed.
 template <int MT, bool KT>
-__device__ __forceinline__ void load_x_global4(const GemvKernelArgs& a, int kb, const uint32_t (&xoff)[MT],
-                                               int lane, half8 (&xa)[MT][4]) {
-  const uint8_t* xb = reinterpret_cast<const uint8_t*>(a.x) + (int64_t)kb * (kTileK4 * 2);
+__device__ __forceinline__ void load_x_global4(const GemvKernelArgs& a, int kb,
+                                               const uint8_t* const (&xrow)[MT],
+                                               const uint32_t (&xoff)[MT], int lane,
+                                               half8 (&xa)[MT][4]) {
   const int k = kb * kTileK4 + 32 * (lane >> 4);
   const int d = KT ? (min(k, a.K - 32) - k) * 2 : 0;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint8_t* xb = xrow[mt] + (int64_t)kb * (kTileK4 * 2);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const half8 v = as_half8(load_u4(xb + xoff[mt] + d + 16 * c));
       xa[mt][c] = (!KT || k < a.K) ? v : half8{};
     }
+  }
 }
 
 // The same fragment read from the LDS copy of x (row pitch `pitch` bytes,
@@ -331,10 +339,17 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
     wstrip[s] = P_w + ((int64_t)strip * a.kblocks + kb0) * kTileBytes;
   }
   const uint32_t woff = lane * 16;
+  // Activation rows: a wave-uniform base per m-tile (its first row, clamped
+  // to M-1) and a per-lane offset of at most 15 rows (load_x_global).
+  const uint8_t* xrow[MT];
   uint32_t xoff[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-    xoff[mt] = (uint32_t)(min(mt * 16 + (lane & 15), a.M - 1) * a.ldx * 2) + (WF ? 64 : 32) * (lane >> 4);
+  for (int mt = 0; mt < MT; ++mt) {
+    const int r0 = min(mt * 16, a.M - 1);
+    xrow[mt] = reinterpret_cast<const uint8_t*>(a.x + (int64_t)r0 * a.ldx);
+    xoff[mt] = (uint32_t)((int64_t)(min(mt * 16 + (lane & 15), a.M - 1) - r0) * a.ldx * 2) +
+               (WF ? 64 : 32) * (lane >> 4);
+  }
   // Group-wise int4 scale of lane l, strip s, tile kl: scale row
   // (4*(kb0 + kl) + l/16) >> gshift (4 lane groups of 32 positions per
   // tile), column 16*strip + l%16.  Wave-uniform row part per tile, fixed
@@ -387,9 +402,9 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
         }
       }
       if constexpr (WF != kWfInt8) {
-        if (!XL) load_x_global4<MT, KT>(a, kb0 + klc, xoff, lane, xv[XL ? 0 : u]);
+        if (!XL) load_x_global4<MT, KT>(a, kb0 + klc, xrow, xoff, lane, xv[XL ? 0 : u]);
       } else if (!XL) {
-        load_x_global<MT, KT>(a, kb0 + klc, xoff, lane, xv[XL ? 0 : u]);
+        load_x_global<MT, KT>(a, kb0 + klc, xrow, xoff, lane, xv[XL ? 0 : u]);
       }
     }
   };

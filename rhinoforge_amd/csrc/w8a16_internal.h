@@ -63,6 +63,18 @@ struct DeviceInfo {
 int device_info(DeviceInfo* out);
 
 GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev);
+
+// The GEMV addresses activations as a 64-bit base per 16-row m-tile plus a
+// per-lane 32-bit byte offset spanning at most 15 rows (and 256 bytes of
+// lane-group and chunk offsets): true when that offset cannot overflow.
+inline bool gemv_offsets_fit(int64_t M, int64_t ldx) {
+  const uint64_t rows = (uint64_t)((M < 16 ? M : 16) - 1);
+  return rows * (uint64_t)ldx * 2u + 256u < (1ull << 32);
+}
+// True when the 32-bit tile offsets of the GEMM kernels fit for this plan
+// and row stride (otherwise int8 launches take the 64-bit-address kernel;
+// int4 launches have none).
+bool gemm_offsets_fit(const GemmPlan& p, int64_t ldx, int K, bool int4);
 // int4: packed-int4 weights (TILE16X128_I4) take the large-tile rules only.
 GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
                    bool int4 = false);

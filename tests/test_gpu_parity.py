@@ -153,31 +153,48 @@ def test_cfg1_qwen3_8b_decode_layer(m):
 
 @pytest.mark.parametrize("m", [1, 32, 512])
 def test_cfg4_qwen3_vl_32b_projections(m):
+    """Every row of every projection against the CPU path (fp16 dequant, fp32
+    BLAS on the host) and the fp64 oracle."""
     for proj, (n, k) in QWEN3_VL_32B.items():
         _say(f"cfg4 M={m} {proj} N={n} K={k}")
         x, q, s, b = make_case(m, n, k, seed=4, outlier=0.01)
-        rows = None if m <= 32 else np.random.default_rng(m).choice(m, 96, replace=False)
-        assert_parity(run_gpu(x, q, s, b), x, q, s, b, rows=rows, label=f"cfg4 M={m} {proj}")
+        assert_parity(run_gpu(x, q, s, b), x, q, s, b, label=f"cfg4 M={m} {proj}")
 
 
 def test_cfg3_qwen3_8b_prefill_mlp():
+    """Each MLP projection alone, every row against the CPU path and the fp64 oracle."""
     m = 2048
     for proj in ("gate", "up", "down"):
         n, k = QWEN3_8B[proj]
         _say(f"cfg3 M={m} {proj} N={n} K={k}")
         x, q, s, b = make_case(m, n, k, seed=3)
         assert rf.select_kernel(m, n, k) == rf.KERNEL_GEMM
-        y = run_gpu(x, q, s, b)
-        rows = np.random.default_rng(3).choice(m, 128, replace=False)
-        assert_parity(y, x, q, s, b, rows=rows, label=f"cfg3 {proj} sampled rows")
-        # every row against an fp32 dequantize-then-matmul on the GPU (torch)
-        w32 = _to_dev(q).float() * _to_dev(s).float()[:, None]
-        ref = _to_dev(x).float() @ w32.T.contiguous()
-        yt = _to_dev(y).float()
-        rel = ((yt - ref).abs().max() / ref.pow(2).mean().sqrt()).item()
-        cos = torch.nn.functional.cosine_similarity(yt, ref, dim=1).min().item()
-        _say(f"  all rows vs torch fp32: err/rms={rel:.3g} min_row_cos={cos:.8f}")
-        assert rel <= 1e-2 and cos >= 0.9999
+        assert_parity(run_gpu(x, q, s, b), x, q, s, b, label=f"cfg3 {proj} all rows")
+
+
+def test_cfg3_prefill_step_as_benched():
+    """The two launches bench.py times for cfg3: gate and up in one linear_multi
+    launch reading x[:, :4096] of a [2048, 12288] activation buffer (row stride
+    12288), then down over the whole buffer; every row of the three outputs
+    against the CPU path and the fp64 oracle."""
+    m = 2048
+    xfull = o.make_activation(o.derive_seed(3, "bench-step"), m, 12288)
+    xd = _to_dev(xfull)
+    weights = {}
+    for i, proj in enumerate(("gate", "up", "down")):
+        n, k = QWEN3_8B[proj]
+        weights[proj] = make_weights(n, k, seed=300 + i)
+    packed = {p: (rf.pack_weight(_to_dev(q)), _to_dev(s)) for p, (q, s) in weights.items()}
+    _say("cfg3 fused gate/up launch M=2048 N=2x12288 K=4096 ldx=12288")
+    ys = rf.linear_multi(xd[:, :4096], [packed["gate"][0], packed["up"][0]],
+                         [packed["gate"][1], packed["up"][1]])
+    yd = rf.linear(xd, *packed["down"])
+    torch.cuda.synchronize()
+    for proj, y in zip(("gate", "up"), ys):
+        q, s = weights[proj]
+        assert_parity(y.cpu().numpy(), xfull[:, :4096], q, s, None, label=f"bench step {proj}")
+    q, s = weights["down"]
+    assert_parity(yd.cpu().numpy(), xfull, q, s, None, label="bench step down")
 
 
 def _lm_head_weights():
@@ -493,23 +510,102 @@ def test_gemm_split_k_matches_unsplit_order_free():
     assert rep.ok, f"gemm split-K vs gemv: {rep}"
 
 
+def _strided_rows(x, ldx):
+    """x [m, k] copied into rows ldx halves apart (one device allocation)."""
+    m, k = x.shape
+    big = torch.empty((m - 1) * ldx + k, dtype=torch.float16, device=DEV)
+    view = big.as_strided((m, k), (ldx, 1))
+    view.copy_(_to_dev(x))
+    return view
+
+
+def _capi_linear(xv, ldx, packed, sd, y, m, n, k, kernel):
+    """rf_w8a16_linear through ctypes on the current stream; returns the status."""
+    lib = capi.load()
+    ws_bytes = lib.rf_w8a16_workspace_bytes(m, n, k)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=DEV)
+    st = lib.rf_w8a16_linear(xv.data_ptr(), ldx, packed.data_ptr(), capi.LAYOUT_TILE16X64,
+                             sd.data_ptr(), None, y.data_ptr(), n, m, n, k, kernel, ws.data_ptr(),
+                             ws_bytes, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return st
+
+
 def test_gemm_fallback_when_row_stride_overflows_32bit_offsets():
     """Rows 2**24 + 8 halves apart: the 128-row tile spans more than 4 GB, so the
-    GEMM must take its 64-bit-address kernel; results must not change."""
+    GEMM called through the C ABI must take its 64-bit-address kernel; results
+    must not change.  The torch op copies such a view to contiguous rows."""
     m, n, k = 130, 256, 200
     ldx = (1 << 24) + 8
     _say(f"gemm fallback M={m} N={n} K={k} ldx={ldx}")
     x, q, s, b = make_case(m, n, k, seed=19)
-    big = torch.empty((m - 1) * ldx + k, dtype=torch.float16, device=DEV)
-    view = big.as_strided((m, k), (ldx, 1))
-    view.copy_(_to_dev(x))
+    view = _strided_rows(x, ldx)
     packed, sd = rf.pack_weight(_to_dev(q)), _to_dev(s)
-    y = rf.linear(view, packed, sd)
-    torch.cuda.synchronize()
     ref = rf.linear(_to_dev(x), packed, sd)
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    capi.check(_capi_linear(view, ldx, packed, sd, y, m, n, k, capi.KERNEL_GEMM), "gemm fallback")
     assert torch.equal(y, ref)
     assert_parity(y.cpu().numpy(), x, q, s, None, label="gemm fallback")
-    del big, view
+    y2 = rf.linear(view, packed, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, ref)
+    del view
+
+
+@pytest.mark.parametrize("m,kernel", [(64, "gemv"), (64, "auto"), (16, "auto"), (40, "gemv")])
+def test_gemv_rows_far_apart(m, kernel):
+    """Activation rows 2**25 + 8 halves apart: (M-1) * ldx * 2 bytes exceed 2**32,
+    so a per-lane 32-bit offset from row 0 would wrap.  The GEMV addresses each
+    16-row m-tile from its own 64-bit base; called through the C ABI (no copy)
+    it must match the oracle and the contiguous call bit for bit."""
+    n, k = 1024, 512
+    ldx = (1 << 25) + 8
+    _say(f"gemv rows far apart M={m} kernel={kernel} ldx={ldx}")
+    x, q, s, _ = make_case(m, n, k, seed=41 + m)
+    view = _strided_rows(x, ldx)
+    packed, sd = rf.pack_weight(_to_dev(q)), _to_dev(s)
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    capi.check(_capi_linear(view, ldx, packed, sd, y, m, n, k, KERNELS[kernel]), "far rows")
+    ref = torch.empty_like(y)
+    capi.check(_capi_linear(_to_dev(x), k, packed, sd, ref, m, n, k, KERNELS[kernel]), "contig")
+    assert torch.equal(y, ref)
+    assert_parity(y.cpu().numpy(), x, q, s, None, label=f"far rows M={m} {kernel}")
+    # the fused argmax (a GEMV epilogue: compared with the argmax of the GEMV's
+    # own logits) and the torch op on the same view
+    ref_v = torch.empty_like(y)
+    capi.check(_capi_linear(_to_dev(x), k, packed, sd, ref_v, m, n, k, capi.KERNEL_GEMV), "gemv")
+    idx = torch.empty(m, dtype=torch.int32, device=DEV)
+    lib = capi.load()
+    ws_bytes = lib.rf_w8a16_workspace_bytes_argmax(m, n, k)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=DEV)
+    st = lib.rf_w8a16_linear_argmax(view.data_ptr(), ldx, packed.data_ptr(), capi.LAYOUT_TILE16X64,
+                                    sd.data_ptr(), None, None, 0, idx.data_ptr(), m, n, k,
+                                    ws.data_ptr(), ws_bytes,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    capi.check(st, "argmax far rows")
+    torch.cuda.synchronize()
+    assert torch.equal(idx, _argmax_first(ref_v))
+    assert torch.equal(rf.linear(view, packed, sd, kernel=KERNELS[kernel]), ref)
+    del view
+
+
+def test_gemv_refuses_rows_beyond_32bit_reach():
+    """Two rows 2**31 halves apart (4 GB): no 16-row span fits a 32-bit offset.
+    A forced GEMV is refused before launch; AUTO runs the GEMM's 64-bit kernel."""
+    m, n, k = 2, 256, 128
+    ldx = 1 << 31
+    _say(f"gemv beyond reach M={m} ldx={ldx}")
+    x, q, s, _ = make_case(m, n, k, seed=47)
+    view = _strided_rows(x, ldx)
+    packed, sd = rf.pack_weight(_to_dev(q)), _to_dev(s)
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    assert _capi_linear(view, ldx, packed, sd, y, m, n, k, capi.KERNEL_GEMV) == capi.EKERNEL
+    capi.check(_capi_linear(view, ldx, packed, sd, y, m, n, k, capi.KERNEL_AUTO), "auto far")
+    ref = rf.linear(_to_dev(x), packed, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    assert torch.equal(rf.linear(view, packed, sd, kernel=rf.KERNEL_GEMV), ref)
+    del view
 
 
 def test_zero_rows_and_extreme_scales():

@@ -97,6 +97,10 @@ CASES = [
     (520, 25600, 1024, 32), (2048, 12288, 1024, 0), (1024, 12288, 2048, 128),
     # GEMM interleaved schedule (one to two 128x128 tiles per CU), group-wise
     (520, 8192, 1024, 32), (1024, 6144, 1024, 128),
+    # 160 tiles in a 3-way K split, run by the 128x128 tile with B in registers:
+    # splits start at K blocks 0, 43 and 86 (an odd block: the second half of
+    # an int4 tile), per-channel and group-wise
+    (500, 5008, 8192, 0), (500, 5008, 8192, 32),
 ]
 
 
@@ -170,6 +174,42 @@ def test_w4a16_capi_direct_call():
     torch.cuda.synchronize()
     assert st == capi.OK, capi.status_str(st)
     check(y.cpu().numpy(), x, q, s, label="capi direct")
+
+
+@pytest.mark.parametrize("m,ldx,gs", [(64, (1 << 25) + 8, 32), (16, (1 << 25) + 8, 0),
+                                      (130, (1 << 24) + 8, 32)])
+def test_w4a16_rows_far_apart(m, ldx, gs):
+    """Activation rows ldx halves apart, (M-1) * ldx * 2 > 2**32 bytes.  Through
+    the C ABI the GEMV (M <= 64) addresses each 16-row m-tile from its own
+    64-bit base and must equal the contiguous call bit for bit; the int4 GEMM
+    has no 64-bit kernel and refuses (EKERNEL) before launch.  The torch op
+    copies such a view to contiguous rows."""
+    import ctypes
+    n, k = 1024, 512
+    _say(f"w4a16 rows far apart M={m} ldx={ldx} gs={gs}")
+    q, s = make_w4(n, k, gs, 8)
+    x = o8.make_activation(9, m, k)
+    big = torch.empty((m - 1) * ldx + k, dtype=torch.float16, device=DEV)
+    view = big.as_strided((m, k), (ldx, 1))
+    view.copy_(_dev(x))
+    sd, wp = _dev(s), rf.pack_weight_int4(_dev(q))
+    ref = rf.linear_w4a16(_dev(x), wp, sd)
+    lib = capi.load()
+    wsb = lib.rf_w4a16_workspace_bytes(m, n, k)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=DEV)
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    st = lib.rf_w4a16_linear(view.data_ptr(), ldx, wp.data_ptr(), sd.data_ptr(), gs, None,
+                             y.data_ptr(), n, m, n, k, capi.KERNEL_AUTO, ws.data_ptr(), wsb,
+                             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    if m <= 64:
+        assert st == capi.OK, capi.status_str(st)
+        assert torch.equal(y, ref)
+        check(y.cpu().numpy(), x, q, s, label=f"w4 far rows M={m}")
+    else:
+        assert st == capi.EKERNEL, capi.status_str(st)
+    assert torch.equal(rf.linear_w4a16(view, wp, sd), ref)
+    del view, big
 
 
 @pytest.mark.parametrize("m,n,k,gs", [(16, 1024, 8192, 32), (300, 1024, 8192, 0)])
