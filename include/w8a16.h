@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define RF_W8A16_ABI_VERSION 2
+#define RF_W8A16_ABI_VERSION 3
 
 /* Status codes.  The torch op maps each to a RuntimeError with the message
  * from rf_w8a16_status_str (the reference raises TORCH_CHECK before any
@@ -43,7 +43,9 @@ typedef enum rf_w8a16_status {
   RF_W8A16_EWORKSPACE = 4,  /* workspace missing or too small             */
   RF_W8A16_EHIP = 5,        /* HIP runtime error (launch or query)        */
   RF_W8A16_EDEVICE = 6,     /* current device is not gfx950               */
-  RF_W8A16_EKERNEL = 7      /* requested kernel cannot run this shape     */
+  RF_W8A16_EKERNEL = 7,     /* requested kernel cannot run this shape     */
+  RF_W8A16_ESCRATCH = 8     /* shape needs more scratch than the
+                               no-allocation entry point holds            */
 } rf_w8a16_status;
 
 /* Weight layout tags (the analogue of the reference's `partition` record,
@@ -160,6 +162,28 @@ int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed,
 int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w8a16_proj* projs,
                           int32_t count, int64_t M, int64_t K, int32_t kernel, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/* No-allocation variant of rf_w8a16_linear_multi.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments and results as rf_w8a16_linear_multi without
+ * the workspace: the split-K counters and fp32 partials of both kernels live
+ * in a library-owned device array of RF_W8A16_NOALLOC_SCRATCH_BYTES bytes per
+ * GPU (its first RF_W8A16_WS_COUNTER_BYTES bytes the counters), looked up on
+ * the first call on each device and held until the process ends.  It
+ * allocates nothing and calls no allocating routine.
+ *   - A shape whose plan needs more scratch returns RF_W8A16_ESCRATCH before
+ *     any launch (e.g. K-split prefill launches of hundreds of 128x128
+ *     tiles); rf_w8a16_linear_multi with a workspace runs those.
+ *   - Every call on one GPU shares that GPU's array.  Calls that overlap in
+ *     time on one GPU (two streams, two host threads, two graphs replayed
+ *     concurrently) race and must be ordered by the caller.
+ *   - The counters start at zero (the first call on a device also clears
+ *     them with a fill kernel on its stream) and every call leaves them zero. */
+#define RF_W8A16_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int rf_w8a16_linear_multi_noalloc(const void* x, int64_t ldx, int32_t layout,
+                                  const rf_w8a16_proj* projs, int32_t count, int64_t M, int64_t K,
+                                  int32_t kernel, void* stream);
 
 /* Greedy-decode lm_head: index[m] = argmax_n fp16(y[m][n]) of
  * y = x . dequant(w)^T (+ bias), int32, the lowest n among equal maxima (NaN

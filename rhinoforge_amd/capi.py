@@ -20,6 +20,8 @@ EWORKSPACE = 4
 EHIP = 5
 EDEVICE = 6
 EKERNEL = 7
+ESCRATCH = 8
+NOALLOC_SCRATCH_BYTES = 32 << 20
 LAYOUT_ROWMAJOR = 0
 LAYOUT_TILE16X64 = 1
 KERNEL_AUTO = 0
@@ -54,6 +56,9 @@ SIGNATURES = {
     "rf_w8a16_linear_multi": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int32, _c.POINTER(Proj),
                                          _c.c_int32, _c.c_int64, _c.c_int64, _c.c_int32,
                                          _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "rf_w8a16_linear_multi_noalloc": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int32,
+                                                 _c.POINTER(Proj), _c.c_int32, _c.c_int64,
+                                                 _c.c_int64, _c.c_int32, _c.c_void_p]),
     "rf_w8a16_linear": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int32,
                                    _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64,
                                    _c.c_int64, _c.c_int64, _c.c_int64, _c.c_int32,

@@ -161,6 +161,55 @@ int auto_kernel_int4(int64_t M) { return M <= 64 ? RF_W8A16_KERNEL_GEMV : RF_W8A
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Scratch of rf_w8a16_linear_multi_noalloc: a fixed device array per GPU
+// (split-K counters, then fp32 partials), so that entry point allocates
+// nothing.  In host code `scratch` is only a stand-in for the symbol: its
+// device address, which differs per GPU, comes from hipGetSymbolAddress on
+// each device and is the only form passed to kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[RF_W8A16_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+__global__ void zero_u4_kernel(uint4* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = make_uint4(0, 0, 0, 0);
+}
+
+// Device address of the current device's scratch array, looked up once per
+// device (with that device current).  The first lookup also clears the
+// counter region with a fill kernel on `stream` (a fill kernel, not a
+// memset node, so that it replays correctly if the first call is captured
+// into a graph); every later call finds the counters zero, because each
+// call leaves them so.
+int noalloc_scratch(hipStream_t stream, void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> ptrs[kMaxDevices];
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return RF_W8A16_EHIP;
+  if (dev < 0 || dev >= kMaxDevices) return RF_W8A16_EDEVICE;
+  void* p = ptrs[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> g(mu);
+    p = ptrs[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RF_W8A16_EHIP;
+      if (!aligned(p, 256)) return RF_W8A16_EHIP;
+      constexpr int n = (int)(RF_W8A16_WS_COUNTER_BYTES / 16);
+      hipLaunchKernelGGL(zero_u4_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                         static_cast<uint4*>(p), n);
+      if (hipGetLastError() != hipSuccess) return RF_W8A16_EHIP;
+      ptrs[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return RF_W8A16_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* rf_w8a16_status_str(int status) {
@@ -178,6 +227,9 @@ const char* rf_w8a16_status_str(int status) {
     case RF_W8A16_EKERNEL:
       return "requested kernel cannot run this shape (GEMV: M > 64, or a row stride ldx whose "
              "32-bit offsets over 16 rows overflow)";
+    case RF_W8A16_ESCRATCH:
+      return "shape needs more split-K scratch than rf_w8a16_linear_multi_noalloc holds "
+             "(RF_W8A16_NOALLOC_SCRATCH_BYTES); call rf_w8a16_linear_multi with a workspace";
     default: return "unknown rf_w8a16 status";
   }
 }
@@ -270,9 +322,12 @@ size_t rf_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return rf_w8a16_workspace_bytes_multi(M, &N, 1, K);
 }
 
-int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w8a16_proj* projs,
-                          int32_t count, int64_t M, int64_t K, int32_t kernel, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+// rf_w8a16_linear_multi and its no-allocation variant (noalloc: the
+// workspace arguments are ignored and the library's scratch array is used).
+static int linear_multi_impl(const void* x, int64_t ldx, int32_t layout,
+                             const rf_w8a16_proj* projs, int32_t count, int64_t M, int64_t K,
+                             int32_t kernel, void* workspace, size_t workspace_bytes, void* stream,
+                             bool noalloc) {
   if (!x || !projs || count < 1 || count > RF_W8A16_MAX_PROJ) return RF_W8A16_EINVAL;
   if (M < 1 || M > kMaxDim || K < 1 || K > kMaxDim || ldx < K) return RF_W8A16_EINVAL;
   for (int i = 0; i < count; ++i) {
@@ -307,6 +362,14 @@ int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w
   if (kernel == RF_W8A16_KERNEL_GEMV && (M > 64 || !rf::gemv_offsets_fit(M, ldx)))
     return RF_W8A16_EKERNEL;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (noalloc) {
+    st = noalloc_scratch(s, &workspace);
+    if (st != RF_W8A16_OK) return st;
+    workspace_bytes = RF_W8A16_NOALLOC_SCRATCH_BYTES;
+  }
+  // A plan needing more workspace than is at hand: the caller's buffer is too
+  // small (EWORKSPACE), or the library's fixed scratch is (ESCRATCH).
+  const int too_small = noalloc ? RF_W8A16_ESCRATCH : RF_W8A16_EWORKSPACE;
 
   rf::LinearProblem pr;
   pr.x = static_cast<const _Float16*>(x);
@@ -333,14 +396,27 @@ int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w
   if (kernel == RF_W8A16_KERNEL_GEMV) {
     const rf::GemvPlan p = rf::plan_gemv(pr.M, n32, count, pr.K, dev);
     if (p.splits > 1 && !workspace_ok(rf::gemv_workspace_bytes(p, pr.M, n32, count)))
-      return RF_W8A16_EWORKSPACE;
+      return too_small;
     e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);
   } else {
     const rf::GemmPlan p = rf::plan_gemm(pr.M, n32, count, pr.K, dev);
-    if (p.splits > 1 && !workspace_ok(rf::gemm_workspace_bytes(p))) return RF_W8A16_EWORKSPACE;
+    if (p.splits > 1 && !workspace_ok(rf::gemm_workspace_bytes(p))) return too_small;
     e = rf::launch_gemm(pr, p, p.splits > 1 ? workspace : nullptr, s);
   }
   return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
+}
+
+int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w8a16_proj* projs,
+                          int32_t count, int64_t M, int64_t K, int32_t kernel, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  return linear_multi_impl(x, ldx, layout, projs, count, M, K, kernel, workspace, workspace_bytes,
+                           stream, false);
+}
+
+int rf_w8a16_linear_multi_noalloc(const void* x, int64_t ldx, int32_t layout,
+                                  const rf_w8a16_proj* projs, int32_t count, int64_t M, int64_t K,
+                                  int32_t kernel, void* stream) {
+  return linear_multi_impl(x, ldx, layout, projs, count, M, K, kernel, nullptr, 0, stream, true);
 }
 
 int rf_w8a16_linear(const void* x, int64_t ldx, const void* w_packed, int32_t layout,

@@ -34,11 +34,11 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(capi.LIB_PATH))
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert capi.load().rf_w8a16_abi_version() == 2
+    assert capi.load().rf_w8a16_abi_version() == 3
 
 
 def test_status_strings():
-    for st in range(0, 8):
+    for st in range(0, 9):
         assert capi.status_str(st)
     assert "unknown" in capi.status_str(99)
 
