@@ -6,6 +6,14 @@ swizzles the weight in place at load time and records the layout on the
 module (runtime/weights.py:386-408, 411-544).  Here the packed weight lives in
 a ``weight`` buffer of shape ``packed_shape(N, K)`` and the layout tag in
 ``self.layout``; forward calls ``torch.ops.w8a16.linear``.
+
+The packed bytes never leave the module under the checkpoint's name: its
+state dict holds ``weight`` as the row-major int8 ``[N, K]`` checkpoint form
+(quant/convert_qwen3.py:65-100), unpacked on save and packed on load.  For
+most shapes packed and row-major tensors have the same dtype and shape, so
+without this a ``state_dict()`` / ``load_state_dict()`` round trip or an HF
+``save_pretrained`` would silently mix the two layouts (the hazard the
+reference guards with its recorded layout, runtime/weights.py:28-49).
 """
 from __future__ import annotations
 
@@ -16,7 +24,46 @@ from . import ops
 from .quant import quantize_linear_per_channel
 
 
-class W8A16Linear(nn.Module):
+class _LogicalWeightStateDict:
+    """State-dict hooks of the packed-weight modules: ``weight`` is saved as
+    the logical int8 [N, K] tensor and packed again on load.  Subclasses give
+    ``_unpack()`` and ``_pack(q)`` and the valid value range."""
+
+    _qmin, _qmax = -128, 127
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        if self.weight.is_meta:
+            destination[prefix + "weight"] = torch.empty(
+                (self.out_features, self.in_features), dtype=torch.int8, device="meta")
+        else:
+            destination[prefix + "weight"] = self._unpack().to(self.weight.device)
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        key = prefix + "weight"
+        logical = state_dict.get(key)
+        if logical is not None:
+            want = (self.out_features, self.in_features)
+            if logical.dtype != torch.int8 or tuple(logical.shape) != want:
+                error_msgs.append(
+                    f"{key}: expected the logical int8 {list(want)} weight (the checkpoint "
+                    f"form; the module packs it), got {logical.dtype} {list(logical.shape)}")
+                return
+            if not logical.is_meta and (int(logical.min()) < self._qmin
+                                        or int(logical.max()) > self._qmax):
+                error_msgs.append(f"{key}: values outside [{self._qmin}, {self._qmax}]")
+                return
+            state_dict[key] = self._pack(logical.to(self.weight.device))
+        try:
+            super()._load_from_state_dict(state_dict, prefix, local_metadata, strict,
+                                          missing_keys, unexpected_keys, error_msgs)
+        finally:
+            if logical is not None:
+                state_dict[key] = logical
+
+
+class W8A16Linear(_LogicalWeightStateDict, nn.Module):
     def __init__(self, in_features: int, out_features: int, bias: bool = False,
                  device=None) -> None:
         super().__init__()
@@ -73,6 +120,11 @@ class W8A16Linear(nn.Module):
         """The int8 [N, K] row-major weight (CPU), e.g. for checkpoint export."""
         return ops.unpack_weight(self.weight, self.out_features, self.in_features)
 
+    _unpack = rowmajor_weight
+
+    def _pack(self, q: torch.Tensor) -> torch.Tensor:
+        return ops.pack_weight(q)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return ops.linear(x, self.weight, self.weight_scale, self.bias, layout=self.layout)
 
@@ -81,7 +133,7 @@ class W8A16Linear(nn.Module):
                 f"bias={self.bias is not None}, layout=TILE16X64")
 
 
-class W4A16Linear(nn.Module):
+class W4A16Linear(_LogicalWeightStateDict, nn.Module):
     """Linear layer with packed int4 weights and fp16 scales (W4A16).
 
     The reference replaces an fp16 ``nn.Linear``'s weight by a packed uint8
@@ -90,7 +142,12 @@ class W4A16Linear(nn.Module):
     (quant/convert_qwen3_w4a16.py:79-121).  Here ``weight`` is the
     TILE16X128_I4 buffer, ``weight_scale`` is ``[N]`` or the logical
     ``[K/group_size, N]``, and forward calls ``torch.ops.w4a16.linear``.
+    The state dict holds ``weight`` as the int4 values in an int8 [N, K]
+    tensor (the reference writes no int4 checkpoint: its conversion is
+    in-memory), packed again on load.
     """
+
+    _qmin, _qmax = -8, 7
 
     def __init__(self, in_features: int, out_features: int, group_size: int | None = 32,
                  bias: bool = False, device=None) -> None:
@@ -161,6 +218,11 @@ class W4A16Linear(nn.Module):
     def rowmajor_weight(self) -> torch.Tensor:
         """The int4 values as an int8 [N, K] tensor (CPU)."""
         return ops.unpack_weight_int4(self.weight, self.out_features, self.in_features)
+
+    _unpack = rowmajor_weight
+
+    def _pack(self, q: torch.Tensor) -> torch.Tensor:
+        return ops.pack_weight_int4(q)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return ops.linear_w4a16(x, self.weight, self.weight_scale, self.bias)

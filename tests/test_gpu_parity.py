@@ -831,6 +831,37 @@ def test_linear_multi_split_k_and_capi():
         assert torch.equal(y, ref)
 
 
+def test_opcheck_on_device_tensors():
+    """torch.library.opcheck with device tensors: schema, autograd registration
+    (the input requires grad; autograd falls through, outputs carry no graph),
+    FakeTensor and AOT dispatch with dynamic shapes, for every compute op."""
+    from torch.library import opcheck
+    n, k = 96, 256
+    x = torch.randn(2, 5, k, device=DEV).half().requires_grad_()
+    q = torch.randint(-128, 128, (n, k), dtype=torch.int8, device=DEV)
+    w, s = rf.pack_weight(q), (torch.rand(n, device=DEV) * 0.01 + 1e-3).half()
+    b = torch.randn(n, device=DEV).half()
+    out = torch.empty(2, 5, n, dtype=torch.float16, device=DEV)
+    q4 = torch.randint(-8, 8, (n, k), dtype=torch.int8, device=DEV)
+    w4, s4 = rf.pack_weight_int4(q4), (torch.rand(k // 32, n, device=DEV) * 0.01 + 1e-3).half()
+    cases = [
+        (torch.ops.w8a16.linear.default, (x, w, s, b)),
+        (torch.ops.w8a16.linear_into.default, (x, w, s, b, out)),
+        (torch.ops.w8a16.linear_multi.default, (x, [w, w], [s, s], [b, None])),
+        (torch.ops.w8a16.linear_argmax.default, (x, w, s, None, True)),
+        (torch.ops.w8a16.pack_weight.default, (q,)),
+        (torch.ops.w4a16.linear.default, (x, w4, s4)),
+        (torch.ops.w4a16.pack_weight.default, (q4,)),
+    ]
+    for op, args in cases:
+        _say(f"opcheck {op}")
+        report = opcheck(op, args, raise_exception=False)
+        failed = {key: v for key, v in report.items() if v != "SUCCESS"}
+        assert not failed, f"{op}: {failed}"
+    y = rf.linear(x, w, s, b)
+    assert not y.requires_grad
+
+
 def test_w8a16_linear_module_forward():
     torch.manual_seed(0)
     lin = torch.nn.Linear(512, 200, bias=True)
