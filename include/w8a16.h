@@ -104,6 +104,34 @@ int rf_w8a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K,
  * (RF_W8A16_KERNEL_GEMV or RF_W8A16_KERNEL_GEMM), or a negative status. */
 int rf_w8a16_select_kernel(int64_t M, int64_t N, int64_t K);
 
+/* Launch plan of one call (host only, nothing is launched): the analogue of
+ * the reference's tile selection select_tile_acc16 / select_tile_acc32
+ * (src/ops/rpu_linear_tiling.h:544-595), which maps (M, local_n, local_k) to
+ * an (m_tile, n_tile) pair. */
+typedef struct rf_w8a16_plan_info {
+  int32_t kernel;           /* RF_W8A16_KERNEL_GEMV or RF_W8A16_KERNEL_GEMM */
+  int32_t tile_m;           /* activation rows per workgroup (GEMV: 16 per m-tile) */
+  int32_t tile_n;           /* output channels per workgroup, per projection */
+  int32_t splits;           /* K splits across workgroups (1: no workspace use) */
+  int32_t waves;            /* wavefronts per workgroup */
+  int32_t workgroups;       /* workgroups of the launch, all splits */
+  uint64_t workspace_bytes; /* workspace the launch uses past the counter region */
+  char name[48];            /* configuration, e.g. "gemm 128x256 B-in-registers" */
+} rf_w8a16_plan_info;
+
+/* Weight formats of rf_w8a16_plan. */
+#define RF_W8A16_FORMAT_INT8 0      /* TILE16X64 int8, per-channel scale        */
+#define RF_W8A16_FORMAT_INT4 1      /* TILE16X128_I4, per-channel scale          */
+#define RF_W8A16_FORMAT_INT4_GROUP 2 /* TILE16X128_I4, group-wise scales        */
+
+/* Plan of a call with `count` projections of widths Ns sharing (M, K) and a
+ * contiguous x (ldx = K), for `kernel` (AUTO / GEMV / GEMM) and weight
+ * `format`, on a part with `cus` compute units (0: the current device's).
+ * Returns RF_W8A16_OK, RF_W8A16_EINVAL or RF_W8A16_EKERNEL (as the compute
+ * entry points would for that shape). */
+int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_t kernel,
+                  int32_t format, int32_t cus, rf_w8a16_plan_info* out);
+
 /* Up to this many projections share one rf_w8a16_linear_multi launch. */
 #define RF_W8A16_MAX_PROJ 4
 

@@ -31,11 +31,24 @@ WS_COUNTER_BYTES = 65536
 MAX_PROJ = 4
 
 
+FORMAT_INT8 = 0
+FORMAT_INT4 = 1
+FORMAT_INT4_GROUP = 2
+
+
 class Proj(ctypes.Structure):
     """struct rf_w8a16_proj (include/w8a16.h)."""
     _fields_ = [("w_packed", ctypes.c_void_p), ("scale", ctypes.c_void_p),
                 ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p),
                 ("ldy", ctypes.c_int64), ("N", ctypes.c_int64)]
+
+
+class PlanInfo(ctypes.Structure):
+    """struct rf_w8a16_plan_info (include/w8a16.h)."""
+    _fields_ = [("kernel", ctypes.c_int32), ("tile_m", ctypes.c_int32),
+                ("tile_n", ctypes.c_int32), ("splits", ctypes.c_int32),
+                ("waves", ctypes.c_int32), ("workgroups", ctypes.c_int32),
+                ("workspace_bytes", ctypes.c_uint64), ("name", ctypes.c_char * 48)]
 
 # name -> (restype, argtypes): every entry point declared in include/w8a16.h
 _c = ctypes
@@ -50,6 +63,8 @@ SIGNATURES = {
     "rf_w8a16_pack_weight_device": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                                _c.c_void_p, _c.c_size_t, _c.c_void_p]),
     "rf_w8a16_select_kernel": (_c.c_int, [_c.c_int64, _c.c_int64, _c.c_int64]),
+    "rf_w8a16_plan": (_c.c_int, [_c.c_int64, _c.POINTER(_c.c_int64), _c.c_int32, _c.c_int64,
+                                 _c.c_int32, _c.c_int32, _c.c_int32, _c.POINTER(PlanInfo)]),
     "rf_w8a16_workspace_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int64]),
     "rf_w8a16_workspace_bytes_multi": (_c.c_size_t, [_c.c_int64, _c.POINTER(_c.c_int64), _c.c_int32,
                                                      _c.c_int64]),
@@ -113,3 +128,20 @@ def status_str(status: int) -> str:
 def check(status: int, what: str) -> None:
     if status != OK:
         raise W8A16Error(status, what)
+
+
+def plan(m: int, ns, k: int, kernel: int = KERNEL_AUTO, fmt: int = FORMAT_INT8,
+         cus: int = 0) -> dict:
+    """The launch plan of a call (rf_w8a16_plan): kernel, tile, K splits,
+    workgroups, workspace bytes and the configuration's name.  ``ns``: the
+    output width, or the widths of projections sharing the input; ``cus``: the
+    compute units to plan for (0: the current device's)."""
+    ns = [int(n) for n in (ns if isinstance(ns, (list, tuple)) else [ns])]
+    arr = (ctypes.c_int64 * len(ns))(*ns)
+    info = PlanInfo()
+    check(load().rf_w8a16_plan(m, arr, len(ns), k, kernel, fmt, cus, ctypes.byref(info)),
+          "rf_w8a16_plan")
+    return {"kernel": "gemv" if info.kernel == KERNEL_GEMV else "gemm", "tile_m": info.tile_m,
+            "tile_n": info.tile_n, "splits": info.splits, "waves": info.waves,
+            "workgroups": info.workgroups, "workspace_bytes": int(info.workspace_bytes),
+            "name": info.name.decode()}

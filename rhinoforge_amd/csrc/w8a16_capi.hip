@@ -8,6 +8,7 @@
 // no core partition to satisfy (runtime/weights.py:97-135), only the
 // 16-byte activation-row alignment of a 128-bit load.
 #include <limits.h>
+#include <stdio.h>
 #include <string.h>
 
 #include <atomic>
@@ -294,6 +295,62 @@ int rf_w8a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K, int64
 int rf_w8a16_select_kernel(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return -RF_W8A16_EINVAL;
   return auto_kernel(M, N, K);
+}
+
+int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_t kernel,
+                  int32_t format, int32_t cus, rf_w8a16_plan_info* out) {
+  if (!out || !Ns || count < 1 || count > RF_W8A16_MAX_PROJ || M < 1 || M > kMaxDim)
+    return RF_W8A16_EINVAL;
+  if (format != RF_W8A16_FORMAT_INT8 && format != RF_W8A16_FORMAT_INT4 &&
+      format != RF_W8A16_FORMAT_INT4_GROUP)
+    return RF_W8A16_EINVAL;
+  const bool int4 = format != RF_W8A16_FORMAT_INT8;
+  if (int4 && count != 1) return RF_W8A16_EINVAL;  // int4 calls take one projection
+  int n32[RF_W8A16_MAX_PROJ];
+  int64_t ntotal = 0;
+  for (int i = 0; i < count; ++i) {
+    if (check_nk(Ns[i], K) != RF_W8A16_OK) return RF_W8A16_EINVAL;
+    n32[i] = (int)Ns[i];
+    ntotal += Ns[i];
+  }
+  rf::DeviceInfo dev;
+  if (cus > 0) {
+    dev.cus = cus;
+    dev.gfx950 = true;
+  } else {
+    const int st = rf::device_info(&dev);
+    if (st != RF_W8A16_OK) return st;
+  }
+  if (kernel == RF_W8A16_KERNEL_AUTO) kernel = int4 ? auto_kernel_int4(M) : auto_kernel(M, ntotal, K);
+  if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
+  if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
+  memset(out, 0, sizeof(*out));
+  out->kernel = kernel;
+  if (kernel == RF_W8A16_KERNEL_GEMV) {
+    const rf::GemvPlan p = int4 ? rf::plan_gemv_int4((int)M, n32[0], (int)K, dev)
+                                : rf::plan_gemv((int)M, n32, count, (int)K, dev);
+    int waves = 0;
+    bool xl = false;
+    rf::gemv_cfg_info(p, (int)M, int4, &waves, &xl);
+    out->tile_m = 16 * p.mt;
+    out->tile_n = 16 * p.ns;
+    out->splits = p.splits;
+    out->waves = waves;
+    out->workgroups = p.groups * p.splits;
+    out->workspace_bytes = rf::gemv_workspace_bytes(p, (int)M, n32, count);
+    snprintf(out->name, sizeof(out->name), "gemv %dx%d strips, %d waves%s", p.mt, p.ns, waves,
+             xl ? ", x in LDS" : "");
+  } else {
+    const rf::GemmPlan p = rf::plan_gemm((int)M, n32, count, (int)K, dev, int4);
+    out->tile_m = p.bm;
+    out->tile_n = p.bn;
+    out->splits = p.splits;
+    out->waves = 4;
+    out->workgroups = p.tiles_m * p.tiles_n * p.splits;
+    out->workspace_bytes = rf::gemm_workspace_bytes(p);
+    snprintf(out->name, sizeof(out->name), "gemm %s", rf::gemm_cfg_name(p.cfg, format, (int)M));
+  }
+  return RF_W8A16_OK;
 }
 
 size_t rf_w8a16_workspace_bytes_multi(int64_t M, const int64_t* Ns, int32_t count, int64_t K) {

@@ -813,11 +813,12 @@ hipError_t launch_dma_t(const GemmKernelArgs& ka, hipStream_t stream) {
 
 // Tile configurations (measured on MI355X over the BASELINE prefill shapes).
 enum GemmCfgId {
-  kV3M128N256,    // 4 wavefronts 1x4, 2 stages, 2 workgroups/CU, B in registers: wide N
-  kV3M128N128,    // 4 wavefronts 1x4, 2 stages, 3 workgroups/CU, B in registers: M >= 1024, N < 8192
-  kV3M128N128S3,  // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: moderate M and N
-  kV3M64N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: small M
-  kV3M256N256,    // (unused: 128x256 with B in registers is faster on every shape measured)
+  kV3M128N256,    // 4 wavefronts 1x4, 2 stages, 2 workgroups/CU, B in registers: wide launches,
+                  // and every launch beyond six 128x128 tiles per CU
+  kV3M128N128,    // 4 wavefronts 1x4, 2 stages, 3 workgroups/CU, B in registers: M >= 1024 up to
+                  // six 128x128 tiles per CU, and K-split launches above one workgroup per CU
+  kV3M128N128S3,  // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: 128 <= M < 1024, N < 16384
+  kV3M64N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: M < 128; wide mid-M launches
   kDmaM128N128,   // 64-bit addresses: when the v3 32-bit offsets could overflow
   kV3M32N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 17..32, with K splits
   kV3M64N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 33..64, with K splits
@@ -827,8 +828,26 @@ enum GemmCfgId {
 
 // {BM, BN, workgroups per CU}
 constexpr int kGemmTile[kGemmCfgCount][3] = {{128, 256, 2}, {128, 128, 3}, {128, 128, 2},
-                                             {64, 256, 2},  {256, 256, 1}, {128, 128, 1},
-                                             {32, 64, 4},   {64, 64, 4},   {128, 128, 3}};
+                                             {64, 256, 2},  {128, 128, 1}, {32, 64, 4},
+                                             {64, 64, 4},   {128, 128, 3}};
+
+// Short description of a configuration as it runs for weight format wf and
+// M rows (group-wise int4 at M >= 1024 runs the interleaved tile's register-B
+// form, see launch_gemm4).
+const char* gemm_cfg_name(int cfg, int wf, int M) {
+  switch (cfg) {
+    case kV3M128N256: return "128x256 B-in-registers";
+    case kV3M128N128: return "128x128 B-in-registers";
+    case kV3M128N128S3: return "128x128 3-stage";
+    case kV3M64N256: return "64x256 3-stage";
+    case kDmaM128N128: return "128x128 64-bit-address";
+    case kV3M32N64: return "32x64 4-stage";
+    case kV3M64N64: return "64x64 4-stage";
+    case kV3M128N128IL:
+      return (wf == kWfInt4Grp && M >= 1024) ? "128x128 B-in-registers" : "128x128 interleaved";
+    default: return "?";
+  }
+}
 
 namespace {
 

@@ -762,6 +762,15 @@ hipError_t launch_gemv4_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStre
 
 }  // namespace
 
+void gemv_cfg_info(const GemvPlan& p, int M, bool int4, int* waves, bool* x_in_lds) {
+  const bool ok = p.cfg >= 0 && p.cfg < kGemvCfgCount;
+  *waves = ok ? kGemvCfgs[p.cfg].w : 0;
+  // int4 stages x in LDS only where its 256 bytes per row and tile fit
+  // (launch_gemv4_cfg)
+  *x_in_lds = ok && kGemvCfgs[p.cfg].xl &&
+              (!int4 || gemv_lds_bytes(1, 1, *waves, true, M, p.kb_per_split, kTileK4) <= 65536);
+}
+
 size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj) {
   if (p.splits <= 1) return 0;
   int64_t np = 0;

@@ -83,6 +83,11 @@ GemvPlan plan_gemv_int4(int M, int N, int K, const DeviceInfo& dev);
 // Workspace bytes past the RF_W8A16_WS_COUNTER_BYTES counter region.
 size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj);
 size_t gemm_workspace_bytes(const GemmPlan& p);
+// Plan descriptions for rf_w8a16_plan: wavefronts per workgroup and x staging
+// of a GEMV configuration; the name of a GEMM configuration as it runs for
+// weight format wf at M rows.
+void gemv_cfg_info(const GemvPlan& p, int M, bool int4, int* waves, bool* x_in_lds);
+const char* gemm_cfg_name(int cfg, int wf, int M);
 
 // Fused argmax of a single-projection GEMV launch (M <= 64): the GEMV
 // stores every workgroup's best 64-bit key per row to `slots` (scratch,

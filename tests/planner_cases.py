@@ -1,0 +1,122 @@
+"""One shape per rule of the kernel planners, with the plan each should get.
+
+Used by test_planner.py (the plan, on the CPU, for a 256-CU part) and by
+test_gpu_parity.py (numerics of the same shapes on the GPU).  Each row is
+(M, N, K, configuration name, tile_m, tile_n, K splits); the names are those
+rf_w8a16_plan reports.
+"""
+
+# GEMV (forced), M <= 64.  tile_m = 16 x m-tiles per wavefront, tile_n = 16 x strips.
+GEMV_POLICY = [
+    # M<=2, >=640 strips: x staged in LDS by DMA
+    (2, 10240, 512, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # same rule, x does not fit in LDS: plain 4-wave config
+    (2, 10240, 16448, "gemv 1x1 strips, 4 waves", 16, 16, 1),
+    # M 3..4, >=640 strips: two strips per 8-wave workgroup
+    (3, 16384, 512, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    (4, 10240, 8256, "gemv 1x2 strips, 8 waves", 16, 32, 1),  # the same at long K
+    # M<=4, 257..639 strips: two strips per workgroup
+    (1, 5000, 320, "gemv 1x2 strips, 16 waves", 16, 32, 1),
+    # M=1, long K: x in LDS, 8 wavefronts
+    (1, 512, 8192, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # M<=4, long K: 8 wavefronts, x from global memory
+    (3, 512, 8192, "gemv 1x1 strips, 8 waves", 16, 16, 1),
+    # M=1, default: x in LDS, 16 wavefronts
+    (1, 512, 4096, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    # same, x copy ends mid-way through a 1 KB DMA chunk
+    (1, 300, 3136, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    # same, K % 64 != 0: x staged through registers, zero past K
+    (1, 520, 3080, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    # M<=4, default (short K, or M > 1)
+    (1, 512, 1024, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # M 5..16, >=2048 strips
+    (8, 32768, 128, "gemv 1x4 strips, 4 waves", 16, 64, 1),
+    # M 5..16, >=1024 strips: two strips per 8-wave workgroup
+    (16, 16384, 256, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 5..16, 640..1023 strips: 4 strips per workgroup
+    (12, 10240, 256, "gemv 1x4 strips, 8 waves", 16, 64, 1),
+    # M 5..16, 257..511 strips: two strips per 16-wave workgroup
+    (10, 5000, 512, "gemv 1x2 strips, 16 waves", 16, 32, 1),
+    # M 5..16, long K: 4-way K split
+    (16, 1024, 8192, "gemv 1x4 strips, 8 waves", 16, 64, 4),
+    # M 5..16, <=64 strips: 4-way K split
+    (9, 1000, 1024, "gemv 1x2 strips, 16 waves", 16, 32, 4),
+    # M 5..16, default
+    (16, 2048, 1024, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # M <= 16, < 640 strips, K >= 16384: 2 strips per workgroup, 8-way split
+    (1, 5120, 16384, "gemv 1x2 strips, 8 waves", 16, 32, 8),
+    (16, 4112, 16456, "gemv 1x2 strips, 8 waves", 16, 32, 8),  # at M 16, ragged N and K
+    # M <= 2, 257..639 strips, K >= 5120: x in LDS
+    (1, 8192, 5120, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # M 3..4, the same strips and K: 2 strips per workgroup
+    (4, 5120, 8192, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 5..16, 512..639 strips: 2 strips per workgroup
+    (12, 8192, 512, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 17..32, >=1024 strips
+    (20, 16384, 128, "gemv 2x4 strips, 4 waves", 32, 64, 1),
+    # M 17..32, long K: 4-way K split
+    (32, 640, 8192, "gemv 2x4 strips, 4 waves", 32, 64, 4),
+    # M 17..32, <=64 strips: 4-way K split
+    (17, 1024, 512, "gemv 2x1 strips, 8 waves", 32, 16, 4),
+    # M 17..32, default
+    (24, 2048, 512, "gemv 2x2 strips, 8 waves", 32, 32, 1),
+    # M 33..64, >=512 strips
+    (40, 8192, 256, "gemv 4x2 strips, 4 waves", 64, 32, 1),
+    # M 33..64, default: 2-way K split
+    (64, 1000, 640, "gemv 4x2 strips, 8 waves", 64, 32, 2),
+]
+
+# GEMM (forced).
+GEMM_POLICY = [
+    # M < 128: 64x256 tiles
+    (100, 520, 1032, "gemm 64x256 3-stage", 64, 256, 1),
+    # M >= 1024, 520 tiles of 128x128 (3 per CU) cost less than 264 of 128x256
+    (1024, 8200, 264, "gemm 128x128 B-in-registers", 128, 128, 1),
+    # 768 tiles of 128x128 (3 per CU): one round of 384 128x256 tiles; K tail
+    (1024, 12288, 200, "gemm 128x256 B-in-registers", 128, 256, 1),
+    # M >= 1024, 768 tiles of 128x256 tie with 1536 of 128x128: 128x256; K tail
+    (1024, 24576, 136, "gemm 128x256 B-in-registers", 128, 256, 1),
+    # M >= 1024, N < 8192: 128x128 tiles, 3 workgroups/CU
+    (1100, 1000, 520, "gemm 128x128 B-in-registers", 128, 128, 1),
+    # the same with 341 tiles (1..2 per CU): interleaved schedule, ragged M/N/K
+    (1300, 3900, 1032, "gemm 128x128 interleaved", 128, 128, 1),
+    # M >= 1024, 8 x 64 = 512 tiles of 128x256 (two whole rounds)
+    (1024, 16384, 128, "gemm 128x256 B-in-registers", 128, 256, 1),
+    # the same rule on ragged M, N, K (9 x 256 = 2304 tiles)
+    (1025, 65300, 72, "gemm 128x256 B-in-registers", 128, 256, 1),
+    # 128 <= M < 1024: 258 tiles of 128x128 (1..2 per CU): interleaved schedule
+    (200, 16400, 136, "gemm 128x128 interleaved", 128, 128, 1),
+    # 128 <= M < 1024: 400 tiles of 128x256 tie with 800 of 128x128: 128x256
+    (500, 25600, 136, "gemm 128x256 B-in-registers", 128, 256, 1),
+    # 128 <= M < 1024, N < 16384: 128x128 tiles, 3 stages
+    (300, 384, 1024, "gemm 128x128 3-stage", 128, 128, 1),
+    # 9 tiles, 64 K blocks: 4-way K split of 16 blocks
+    (300, 384, 4096, "gemm 128x128 3-stage", 128, 128, 4),
+    # 128 tiles, 17 K blocks: too short to split; K tail
+    (512, 4096, 1032, "gemm 128x128 3-stage", 128, 128, 1),
+    # 275 tiles (1..2 per CU): interleaved schedule
+    (640, 7000, 520, "gemm 128x128 interleaved", 128, 128, 1),
+    # 16 tiles, 33 K blocks: 2-way split, K tail in split 1
+    (200, 1000, 2056, "gemm 128x128 3-stage", 128, 128, 2),
+    # M < 128: 6 tiles, 4-way K split
+    (100, 520, 4096, "gemm 64x256 3-stage", 64, 256, 4),
+    # M >= 1024: 128 tiles of 128x128, 5-way K split (>= 24 blocks each)
+    (1024, 2048, 8192, "gemm 128x128 B-in-registers", 128, 128, 5),
+    # 160 tiles, 3-way split (two per CU): 128x128 with B in registers; K tail
+    (500, 5000, 8200, "gemm 128x128 B-in-registers", 128, 128, 3),
+    # 256 tiles (one per CU), K >= 12288: 2-way K split
+    (1024, 4096, 12288, "gemm 128x128 B-in-registers", 128, 128, 2),
+    # M <= 64: 32x64 / 64x64 tiles, split to ~3 workgroups per CU
+    (20, 4096, 4096, "gemm 32x64 4-stage", 32, 64, 8),     # 64 tiles, 8-way (8 K blocks each)
+    (48, 5120, 8192, "gemm 64x64 4-stage", 64, 64, 8),     # M 33..64: 80 tiles, 8-way split
+    # M 33..64, 100 tiles of 64x256 (>= 96): 64x256 with a 2-way K split
+    (40, 25600, 5120, "gemm 64x256 3-stage", 64, 256, 2),
+    # 193 tiles of 64x256 (>= 192): 64x256, no split; ragged N, K tail
+    (24, 49408, 136, "gemm 64x256 3-stage", 64, 256, 1),
+    (64, 1000, 200, "gemm 64x64 4-stage", 64, 64, 1),      # ragged N, 4 K blocks: no split
+    (33, 4104, 520, "gemm 64x64 4-stage", 64, 64, 1),      # ragged M and N, K tail (9 K blocks)
+    # 33 tiles, 25 K blocks: 2-way split, K tail in split 1
+    (17, 2056, 1544, "gemm 32x64 4-stage", 32, 64, 2),
+    # M = 1 forced to the GEMM: 16 tiles of 32x64, 8-way split
+    (1, 1024, 4096, "gemm 32x64 4-stage", 32, 64, 8),
+]

@@ -18,6 +18,7 @@ import torch
 import rhinoforge_amd as rf
 from rhinoforge_amd import capi
 from oracle import w8a16 as o
+import planner_cases
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -392,37 +393,7 @@ def test_edge_shapes(m, n, k, bias):
 
 # One shape per rule of the GEMV planner (w8a16_gemv.hip plan_gemv), so every
 # kernel configuration it can pick runs at least once.
-GEMV_POLICY = [
-    (2, 10240, 512),   # M<=2, >=640 strips: x staged in LDS by DMA
-    (2, 10240, 16448), # same rule, x does not fit in LDS: plain 4-wave config
-    (3, 16384, 512),   # M 3..4, >=640 strips: two strips per 8-wave workgroup
-    (4, 10240, 8256),  # the same at long K
-    (1, 5000, 320),    # M<=4, 257..639 strips: two strips per workgroup
-    (1, 512, 8192),    # M=1, long K: x in LDS, 8 wavefronts
-    (3, 512, 8192),    # M<=4, long K: 8 wavefronts, x from global memory
-    (1, 512, 4096),    # M=1, default: x in LDS, 16 wavefronts
-    (1, 300, 3136),    # same, x copy ends mid-way through a 1 KB DMA chunk
-    (1, 520, 3080),    # same, K % 64 != 0: x staged through registers, zero past K
-    (1, 512, 1024),    # M<=4, default (short K, or M > 1)
-    (8, 32768, 128),   # M 5..16, >=2048 strips
-    (16, 16384, 256),  # M 5..16, >=1024 strips: two strips per 8-wave workgroup
-    (12, 10240, 256),  # M 5..16, 640..1023 strips: 4 strips per WG
-    (10, 5000, 512),   # M 5..16, 257..511 strips: two strips per 16-wave workgroup
-    (16, 1024, 8192),  # M 5..16, long K: 4-way K split
-    (9, 1000, 1024),   # M 5..16, <=64 strips: 4-way K split
-    (16, 2048, 1024),  # M 5..16, default
-    (1, 5120, 16384),  # M <= 16, < 640 strips, K >= 16384: 2 strips per WG, 8-way split
-    (16, 4112, 16456), # the same at M 16, ragged N and K
-    (1, 8192, 5120),   # M <= 2, 257..639 strips, K >= 5120: x in LDS
-    (4, 5120, 8192),   # M 3..4, the same strips and K: 2 strips per WG
-    (12, 8192, 512),   # M 5..16, 512..639 strips: 2 strips per WG
-    (20, 16384, 128),  # M 17..32, >=1024 strips
-    (32, 640, 8192),   # M 17..32, long K: 4-way K split
-    (17, 1024, 512),   # M 17..32, <=64 strips: 4-way K split
-    (24, 2048, 512),   # M 17..32, default
-    (40, 8192, 256),   # M 33..64, >=512 strips
-    (64, 1000, 640),   # M 33..64, default: 2-way K split
-]
+GEMV_POLICY = [row[:3] for row in planner_cases.GEMV_POLICY]  # one shape per GEMV planner rule
 
 
 @pytest.mark.parametrize("m,n,k", GEMV_POLICY)
@@ -442,36 +413,7 @@ def test_gemv_every_planner_rule(m, n, k):
 # 256-CU MI355X: tiles = ceil(M/BM) * ceil(N/BN); a K split below one tile per
 # CU (>= 16 or 24 blocks of 64 per split), or for K >= 12288 at one tile per CU
 # or a CU share of 1.25..1.75 / 2.25..2.75 tiles.
-GEMM_POLICY = [
-    (100, 520, 1032),    # M < 128: 64x256 tiles
-    (1024, 8200, 264),   # M >= 1024, 520 tiles of 128x128 (3 per CU) cost less than 264 of 128x256
-    (1024, 12288, 200),  # 768 tiles of 128x128 (3 per CU): one round of 384 128x256 tiles; K tail
-    (1024, 24576, 136),  # M >= 1024, 768 tiles of 128x256 tie with 1536 of 128x128: 128x256; K tail
-    (1100, 1000, 520),   # M >= 1024, N < 8192: 128x128 tiles, 3 workgroups/CU
-    (1300, 3900, 1032),  # the same with 341 tiles (1..2 per CU): interleaved schedule, ragged M/N/K
-    (1024, 16384, 128),  # M >= 1024, 8 x 64 = 512 tiles of 128x256 (two whole rounds)
-    (1025, 65300, 72),   # the same rule on ragged M, N, K (5 x 256 = 1280 tiles)
-    (200, 16400, 136),   # 128 <= M < 1024: 258 tiles of 128x128 (1..2 per CU): interleaved schedule
-    (500, 25600, 136),   # 128 <= M < 1024: 400 tiles of 128x256 tie with 800 of 128x128: 128x256
-    (300, 384, 1024),    # 128 <= M < 1024, N < 16384: 128x128 tiles, 3 stages
-    (300, 384, 4096),    # 9 tiles, 64 K blocks: 4-way K split of 16 blocks
-    (512, 4096, 1032),   # 128 <= M < 1024: 128 tiles, 17 K blocks: too short to split; K tail
-    (640, 7000, 520),    # 128 <= M < 1024: 275 tiles (1..2 per CU), interleaved schedule
-    (200, 1000, 2056),   # 16 tiles, 33 K blocks: 2-way split, K tail in split 1
-    (100, 520, 4096),    # M < 128: 6 tiles, 4-way K split
-    (1024, 2048, 8192),  # M >= 1024: 128 tiles of 128x128, 5-way K split (>= 24 blocks each)
-    (500, 5000, 8200),   # 160 tiles, 3-way split (two per CU): 128x128 with B in registers; K tail
-    (1024, 4096, 12288), # 256 tiles (one per CU), K >= 12288: 2-way K split
-    # M <= 64: 32x64 / 64x64 tiles, split to ~3 workgroups per CU
-    (20, 4096, 4096),    # M 17..32: 64 tiles, 8-way split (8 K blocks each)
-    (48, 5120, 8192),    # M 33..64: 80 tiles, 8-way split
-    (40, 25600, 5120),   # M 33..64, 100 tiles of 64x256 (>= 96): 64x256 with a 2-way K split
-    (24, 49408, 136),    # 193 tiles of 64x256 (>= 192): 64x256, no split; ragged N, K tail
-    (64, 1000, 200),     # ragged N, 4 K blocks: no split
-    (33, 4104, 520),     # ragged M and N, K tail (9 K blocks): no split
-    (17, 2056, 1544),    # 33 tiles, 25 K blocks: 2-way split, K tail in split 1
-    (1, 1024, 4096),     # M = 1 forced to the GEMM: 16 tiles of 32x64, 8-way split
-]
+GEMM_POLICY = [row[:3] for row in planner_cases.GEMM_POLICY]  # one shape per GEMM planner rule
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_POLICY)
