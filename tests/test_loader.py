@@ -86,7 +86,7 @@ def test_converter_refuses_overwrite_and_copies_int8(ckpts, tmp_path):
         convert.convert_checkpoint(ckpts / "src", ckpts / "dst", log=lambda *a: None)
     stats = convert.convert_checkpoint(ckpts / "dst", tmp_path / "again", skip_modules=[],
                                        log=lambda *a: None)
-    assert stats["n_quantized"] == 0
+    assert stats["quantized"] == 0
     a, b = read_all(ckpts / "dst"), read_all(tmp_path / "again")
     assert a.keys() == b.keys() and all(torch.equal(a[k], b[k]) for k in a)
 
@@ -187,15 +187,15 @@ def _rewrite(path: Path, fn) -> None:
 
 
 @pytest.mark.parametrize("case,exc,match", [
-    ("drop_scale", KeyError, "without fp16 weight_scale"),
-    ("fp32_scale", TypeError, "must be fp16"),
-    ("short_scale", ValueError, "has shape"),
-    ("extra_tensor", KeyError, "no matching model parameter"),
-    ("drop_norm", KeyError, "did not provide"),
-    ("orphan_scale", KeyError, "without an int8 weight"),
-    ("float_projection", KeyError, "projection inventory mismatch"),
-    ("int32_tensor", TypeError, "must be floating"),
-    ("wrong_shape", ValueError, "has shape"),
+    ("drop_scale", KeyError, "with no fp16 scale"),
+    ("fp32_scale", TypeError, "scales are fp16"),
+    ("short_scale", ValueError, "one entry per weight row"),
+    ("extra_tensor", KeyError, "has no parameter of that name"),
+    ("drop_norm", KeyError, "absent from the checkpoint"),
+    ("orphan_scale", KeyError, "no int8 weight beside it"),
+    ("float_projection", KeyError, "differ from what quant_config implies"),
+    ("int32_tensor", TypeError, "floating tensors only"),
+    ("wrong_shape", ValueError, "checkpoint shape"),
 ])
 def test_loader_refuses_bad_checkpoints(ckpts, tmp_path, case, exc, match):
     d = _copy(ckpts / "dst", tmp_path / case)
@@ -244,7 +244,7 @@ def test_loader_refuses_index_mismatch(tmp_path):
     other = [s for s in sorted(set(idx["weight_map"].values())) if s != idx["weight_map"][name]]
     idx["weight_map"][name] = other[0]
     idx_path.write_text(json.dumps(idx))
-    with pytest.raises(KeyError, match="index maps"):
+    with pytest.raises(KeyError, match="index puts"):
         load.load_w8a16_model(None, tmp_path / "dst", device="cpu")
 
 
@@ -341,7 +341,7 @@ def test_qwen3_vl_checkpoint_loads_with_text_projections_swapped(tmp_path):
     transformers.Qwen3VLForConditionalGeneration(cfg).save_pretrained(
         tmp_path / "src", safe_serialization=True)
     stats = convert.convert_checkpoint(tmp_path / "src", tmp_path / "dst", log=lambda *a: None)
-    assert stats["n_quantized"] == 2 * 7
+    assert stats["quantized"] == 2 * 7
     model = load.load_w8a16_model(None, tmp_path / "dst", device="cpu")
     assert type(model).__name__ == "Qwen3VLForConditionalGeneration"
     assert load.detect_and_validate_decoder_w8a16(model.model.language_model)
