@@ -1,44 +1,64 @@
-"""Per-channel symmetric W8A16 quantizer and dequantizer (torch).
+"""Symmetric per-output-channel quantizer for W8A16 checkpoints (torch).
 
-Same contract as the reference's converter helpers
-(python/rpu_backend/quant/_common.py:10-41): int8 storage plus one fp16 scale
-per output channel, computed as
+Byte-identical to what the reference's converters write
+(python/rpu_backend/quant/_common.py:10-41), so a checkpoint converted here
+loads there and vice versa.  For a weight row ``w`` and ``L = 2**(bits-1)``:
 
-    w16   = fp16(w)                                  # cast before amax (:28)
-    amax  = max_k |f32(w16)|                         # (:29)
-    scale = max(fp16(amax / qmax), fp16 tiny 2**-14) # (:30)
-    q     = clamp(round_half_even(f32(w16) / f32(scale)), qmin, qmax)   # (:31-35)
+    w16   = fp16(w)                              the row is cast first
+    amax  = max |f32(w16)|
+    scale = max(fp16(amax / (L - 1)), 2**-14)    fp16, never below fp16 tiny
+    q     = clamp(rint(f32(w16) / f32(scale)), -L, L - 1)     ties to even
 
-These run on whatever device the tensor lives on (division and rounding are
-IEEE-exact, so CPU and GPU results are bit-identical).
+Division and rounding are correctly rounded IEEE operations, so the CPU and a
+HIP device produce the same bytes.  The int4 quantizers in ``int4`` reuse the
+scale and rounding steps below.
 """
 from __future__ import annotations
 
 import torch
 
-_FP16_TINY = torch.finfo(torch.float16).tiny
+_FP16_TINY = torch.finfo(torch.float16).tiny   # 2**-14, the smallest normal fp16
+
+
+def signed_levels(bits: int) -> tuple[int, int]:
+    """(lowest, highest) integer a ``bits``-wide two's-complement value takes;
+    4- and 8-bit values are supported, both kept in int8 containers."""
+    if bits not in (4, 8):
+        raise ValueError(f"bits={bits}: values are 4 or 8 bits wide (stored in int8)")
+    half = 1 << (bits - 1)
+    return -half, half - 1
+
+
+def scale_from_amax(amax: torch.Tensor, top: int) -> torch.Tensor:
+    """fp16 step that maps ``amax`` (fp32) onto level ``top``, floored at fp16 tiny."""
+    return (amax / float(top)).to(torch.float16).clamp_min(_FP16_TINY)
+
+
+def round_to_levels(w32: torch.Tensor, step16: torch.Tensor, lo: int, hi: int) -> torch.Tensor:
+    """int8 ``clamp(rint(w32 / f32(step16)), lo, hi)``; ``step16`` broadcasts against ``w32``."""
+    return torch.round(w32 / step16.to(torch.float32)).clamp_(lo, hi).to(torch.int8)
+
+
+def _as_matrix(weight: torch.Tensor) -> torch.Tensor:
+    if weight.dim() != 2:
+        raise ValueError(f"a linear weight is a 2-D [out_features, in_features] matrix; "
+                         f"this one has shape {tuple(weight.shape)}")
+    return weight.detach()
 
 
 def quantize_linear_per_channel(weight: torch.Tensor, *, bits: int = 8
                                 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Quantize a Linear weight [N, K] to int8 storage plus a per-row fp16 scale.
+    """[N, K] floating weight -> (int8 [N, K] values, fp16 [N] step per row).
 
-    ``bits=4`` stores signed 4-bit values in int8 containers (the reference's
-    fake-W4 probe format); nibbles are not packed.
+    With ``bits=4`` the values lie in [-8, 7] but are still one per int8 (the
+    reference's fake-W4 checkpoint form); nothing is packed into nibbles.
     """
-    if weight.dim() != 2:
-        raise ValueError(f"expected 2-D Linear weight, got {tuple(weight.shape)}")
-    if bits not in (4, 8):
-        raise ValueError(f"expected bits to be 4 or 8, got {bits}")
-    qmax = (1 << (bits - 1)) - 1
-    qmin = -(1 << (bits - 1))
-    w32 = weight.detach().to(torch.float16).to(torch.float32)
-    amax = w32.abs().amax(dim=1)
-    scale = (amax / float(qmax)).to(torch.float16).clamp_min(_FP16_TINY)
-    q = torch.round(w32 / scale.to(torch.float32).unsqueeze(1)).clamp_(qmin, qmax).to(torch.int8)
-    return q, scale
+    lo, hi = signed_levels(bits)
+    w32 = _as_matrix(weight).to(torch.float16).to(torch.float32)
+    step = scale_from_amax(w32.abs().amax(dim=1), hi)
+    return round_to_levels(w32, step.unsqueeze(1), lo, hi), step
 
 
 def dequantize_linear_per_channel(w_int8: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
-    """fp16(scale)[:, None] * fp16(q), i.e. RN_fp16(s*q) elementwise."""
+    """fp16 [N, K] weight ``RN_fp16(scale[n] * q[n, k])`` (one fp16 multiply)."""
     return scale.to(torch.float16).unsqueeze(1) * w_int8.to(torch.float16)
