@@ -820,16 +820,19 @@ enum GemmCfgId {
   kV3M128N128S3,  // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: 128 <= M < 1024, N < 16384
   kV3M64N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: M < 128; wide mid-M launches
   kDmaM128N128,   // 64-bit addresses: when the v3 32-bit offsets could overflow
-  kV3M32N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 17..32, with K splits
+  kV3M32N64,      // 4 wavefronts 1x4, 3 stages, 4 workgroups/CU: M <= 32, with K splits
   kV3M64N64,      // 4 wavefronts 1x4, 4 stages, 4 workgroups/CU: M 33..64, with K splits
   kV3M128N128IL,  // kV3M128N128 with the interleaved MFMA schedule: 1..2 tiles per CU
+  kV3M32N128,     // 4 wavefronts 1x4, 4 stages, 3 workgroups/CU: M <= 32, >= 0.75 tiles per CU
+  kV3M32N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: M <= 32, >= 0.75 tiles per CU
   kGemmCfgCount
 };
 
 // {BM, BN, workgroups per CU}
 constexpr int kGemmTile[kGemmCfgCount][3] = {{128, 256, 2}, {128, 128, 3}, {128, 128, 2},
                                              {64, 256, 2},  {128, 128, 1}, {32, 64, 4},
-                                             {64, 64, 4},   {128, 128, 3}};
+                                             {64, 64, 4},   {128, 128, 3}, {32, 128, 3},
+                                             {32, 256, 2}};
 
 // Short description of a configuration as it runs for weight format wf and
 // M rows (group-wise int4 at M >= 1024 runs the interleaved tile's register-B
@@ -841,10 +844,12 @@ const char* gemm_cfg_name(int cfg, int wf, int M) {
     case kV3M128N128S3: return "128x128 3-stage";
     case kV3M64N256: return "64x256 3-stage";
     case kDmaM128N128: return "128x128 64-bit-address";
-    case kV3M32N64: return "32x64 4-stage";
+    case kV3M32N64: return "32x64 3-stage";
     case kV3M64N64: return "64x64 4-stage";
     case kV3M128N128IL:
       return (wf == kWfInt4Grp && M >= 1024) ? "128x128 B-in-registers" : "128x128 interleaved";
+    case kV3M32N128: return "32x128 4-stage";
+    case kV3M32N256: return "32x256 3-stage";
     default: return "?";
   }
 }
@@ -890,13 +895,50 @@ void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
 // over (M, total N) tuned on MI355X, plus a K split when the output has
 // fewer tiles than the chip has workgroup slots.
 //
-// M <= 64 (int8): small tiles (32x64 or 64x64, four per CU) and a K split
-// that brings the launch to about three workgroups per CU -- the largest
-// power of two <= 768 / tiles, at most 8, each split at least 8 K blocks
-// (measured on the Qwen3-8B / Qwen3-VL-32B shapes at M 32..64; with the
-// 64x256 tile these launches had 16..100 workgroups).
+// M <= 32 (int8): one tile row of 32.  The widest tile that still gives
+// >= 0.75 tiles per CU runs unsplit (32x256, then 32x128): every tile
+// streams its weight strips once and re-reads the M x K activation panel,
+// so wider tiles cut that re-read.  Otherwise 32x64 tiles with a 4-way K
+// split (8-way from 192 K blocks), fewer when a split would hold < 8 K
+// blocks or the launch exceed three workgroups per CU.  (MI355X, four
+// rotated weight copies, M = 32: Qwen3-VL-32B gate 25600 x 5120 28.3 us on
+// 200 32x128 tiles instead of 31.9 on 400 32x64; fused gate/up 51200 x 5120
+// 50.4 instead of 53.0 us with 64x256; fused q/k/v 10240 x 5120 13.8 us and
+// o 5120 x 8192 13.2 us with 4 splits instead of 14.6 / 14.2 us with the
+// previous 4-stage tile or 8 splits; Qwen3-8B o 4096 x 4096 9.3 instead of
+// 10.2 us; down 5120 x 25600 34.6 us with 8 splits.)
+//
+// M 33..64 (int8): 64x64 tiles (four per CU) and a K split that brings the
+// launch to about three workgroups per CU -- the largest power of two <= 768
+// / tiles, at most 8, each split at least 8 K blocks -- or 64x256 tiles on
+// wide launches.
 GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev, bool int4) {
   const int cus = dev.cus > 0 ? dev.cus : 256;
+  if (M <= 32 && !int4) {
+    GemmPlan p;
+    const int kblocks = (int)ceil_div(K, 64);
+    int64_t t256 = 0, t128 = 0;
+    for (int i = 0; i < nproj; ++i) {
+      t256 += ceil_div(Ns[i], 256);
+      t128 += ceil_div(Ns[i], 128);
+    }
+    if (4 * t256 >= 3LL * cus || 4 * t128 >= 3LL * cus) {
+      p.cfg = 4 * t256 >= 3LL * cus ? kV3M32N256 : kV3M32N128;
+      set_tiles(p, M, Ns, nproj);
+      p.splits = 1;
+      p.kb_per_split = kblocks;
+      return p;
+    }
+    p.cfg = kV3M32N64;
+    set_tiles(p, M, Ns, nproj);
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    int s = kblocks >= 192 ? 8 : 4;
+    while (s > 1 && (s * tiles > 3LL * cus || kblocks < 8 * s)) s /= 2;
+    if (tiles > kMaxSplitTiles) s = 1;
+    p.kb_per_split = (int)ceil_div(kblocks, s);
+    p.splits = (int)ceil_div(kblocks, p.kb_per_split);
+    return p;
+  }
   if (M <= 64 && !int4) {
     GemmPlan p;
     const int kblocks = (int)ceil_div(K, 64);
@@ -904,20 +946,20 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
     // activation traffic is (tile columns) x M x K x 2 bytes -- as large as
     // the weights themselves with 64-column tiles at N = 51200.  64x256 tiles
     // read it a quarter as often: taken when they alone give >= 0.75
-    // workgroups per CU, or from M = 33 with a 2-way K split at >= 0.375
+    // workgroups per CU, or with a 2-way K split at >= 0.375
     // (Qwen3-VL-32B gate/up at M 32..64: 52..57 us instead of 63..84 us;
     // Qwen3-8B gate/up at M 48..64: 28.5 instead of 30.5..32 us; MI355X).
     int64_t w256 = 0;
     for (int i = 0; i < nproj; ++i) w256 += ceil_div(Ns[i], 256);
     const bool wide = w256 * 4 >= 3LL * cus;
-    if (wide || (M > 32 && w256 * 8 >= 3LL * cus && kblocks >= 2 * kMinKbPerSplit)) {
+    if (wide || (w256 * 8 >= 3LL * cus && kblocks >= 2 * kMinKbPerSplit)) {
       p.cfg = kV3M64N256;
       set_tiles(p, M, Ns, nproj);
       p.kb_per_split = wide ? kblocks : (int)ceil_div(kblocks, 2);
       p.splits = (int)ceil_div(kblocks, p.kb_per_split);
       return p;
     }
-    p.cfg = M <= 32 ? kV3M32N64 : kV3M64N64;
+    p.cfg = kV3M64N64;
     set_tiles(p, M, Ns, nproj);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     int s = 1;
@@ -1107,9 +1149,11 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
     case kV3M128N128S3: return launch_v3_t<128, 128, 1, 4, 3, 2>(ka, stream);
     case kV3M64N256: return launch_v3_t<64, 256, 1, 4, 3, 2>(ka, stream);
     case kDmaM128N128: return launch_dma_t<128, 128, 1, 4, 3>(ka, stream);
-    case kV3M32N64: return launch_v3_t<32, 64, 1, 4, 4, 4>(ka, stream);
+    case kV3M32N64: return launch_v3_t<32, 64, 1, 4, 3, 4>(ka, stream);
     case kV3M64N64: return launch_v3_t<64, 64, 1, 4, 4, 4>(ka, stream);
     case kV3M128N128IL: return launch_v3_t<128, 128, 1, 4, 2, 3, kWfInt8, true>(ka, stream);
+    case kV3M32N128: return launch_v3_t<32, 128, 1, 4, 4, 3>(ka, stream);
+    case kV3M32N256: return launch_v3_t<32, 256, 1, 4, 3, 2>(ka, stream);
     default: return hipErrorInvalidValue;
   }
 }

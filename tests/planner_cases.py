@@ -106,17 +106,24 @@ GEMM_POLICY = [
     (500, 5000, 8200, "gemm 128x128 B-in-registers", 128, 128, 3),
     # 256 tiles (one per CU), K >= 12288: 2-way K split
     (1024, 4096, 12288, "gemm 128x128 B-in-registers", 128, 128, 2),
-    # M <= 64: 32x64 / 64x64 tiles, split to ~3 workgroups per CU
-    (20, 4096, 4096, "gemm 32x64 4-stage", 32, 64, 8),     # 64 tiles, 8-way (8 K blocks each)
-    (48, 5120, 8192, "gemm 64x64 4-stage", 64, 64, 8),     # M 33..64: 80 tiles, 8-way split
+    # M <= 32: 32x64 tiles, 4-way K split (16 K blocks each)
+    (20, 4096, 4096, "gemm 32x64 3-stage", 32, 64, 4),
+    # M <= 32, K >= 192 blocks: 8-way split
+    (32, 4096, 12288, "gemm 32x64 3-stage", 32, 64, 8),
+    # M <= 32, 200 tiles of 32x128 (>= 192), 100 of 32x256: 32x128, no split
+    (32, 25600, 320, "gemm 32x128 4-stage", 32, 128, 1),
+    # M <= 32, 193 tiles of 32x256 (>= 192): 32x256, no split; ragged N, K tail
+    (24, 49408, 136, "gemm 32x256 3-stage", 32, 256, 1),
+    # M <= 32, 33 tiles, 25 K blocks: 2-way split (4 would leave < 8 blocks), K tail in split 1
+    (17, 2056, 1544, "gemm 32x64 3-stage", 32, 64, 2),
+    # M = 1 forced to the GEMM: 16 tiles of 32x64, 4-way split
+    (1, 1024, 4096, "gemm 32x64 3-stage", 32, 64, 4),
+    # M 33..64: 64x64 tiles, split to ~3 workgroups per CU
+    (48, 5120, 8192, "gemm 64x64 4-stage", 64, 64, 8),     # 80 tiles, 8-way split
     # M 33..64, 100 tiles of 64x256 (>= 96): 64x256 with a 2-way K split
     (40, 25600, 5120, "gemm 64x256 3-stage", 64, 256, 2),
-    # 193 tiles of 64x256 (>= 192): 64x256, no split; ragged N, K tail
-    (24, 49408, 136, "gemm 64x256 3-stage", 64, 256, 1),
+    # M 33..64, 193 tiles of 64x256 (>= 192): 64x256, no split; ragged N, K tail
+    (40, 49408, 136, "gemm 64x256 3-stage", 64, 256, 1),
     (64, 1000, 200, "gemm 64x64 4-stage", 64, 64, 1),      # ragged N, 4 K blocks: no split
     (33, 4104, 520, "gemm 64x64 4-stage", 64, 64, 1),      # ragged M and N, K tail (9 K blocks)
-    # 33 tiles, 25 K blocks: 2-way split, K tail in split 1
-    (17, 2056, 1544, "gemm 32x64 4-stage", 32, 64, 2),
-    # M = 1 forced to the GEMM: 16 tiles of 32x64, 8-way split
-    (1, 1024, 4096, "gemm 32x64 4-stage", 32, 64, 8),
 ]
