@@ -872,8 +872,15 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
       if (!lds_fits(cfg, M, kblocks)) cfg = kG1x1W4U4;
     } else if (strips_ge(257)) {
       cfg = kG1x2W16U2;
-    } else if (kblocks >= 128) {
+    } else if (kblocks >= 128 || (M == 1 && kblocks >= 80)) {
+      // (at M = 1 from K = 5120: ten tiles per wavefront instead of five,
+      // Qwen3-VL-32B k/v 1024 x 5120 4.84 instead of 5.15 us)
       cfg = (M == 1 && lds_fits(kG1x1W8U4XL, M, kblocks)) ? kG1x1W8U4XL : kG1x1W8U4;
+    } else if (kblocks <= 16) {
+      // K <= 1024: four wavefronts of four tiles, one pipeline stage each,
+      // and a 4-way cross-wavefront sum instead of 16 (Qwen3-0.6B q/k/v
+      // 3072 x 1024 at M 1 / 4: 3.12 / 3.24 us instead of 3.61 / 3.77 us).
+      cfg = kG1x1W4U4;
     } else {
       // (short K: one tile per wavefront does not amortize the staging wait)
       cfg = (M == 1 && kblocks >= 48 && lds_fits(kG1x1W16U4XL, M, kblocks)) ? kG1x1W16U4XL

@@ -27,8 +27,13 @@ GEMV_POLICY = [
     (1, 300, 3136, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
     # same, K % 64 != 0: x staged through registers, zero past K
     (1, 520, 3080, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    # M<=4, K <= 1024: four wavefronts of four tiles
+    (1, 3072, 1024, "gemv 1x1 strips, 4 waves", 16, 16, 1),
+    (4, 512, 1000, "gemv 1x1 strips, 4 waves", 16, 16, 1),   # ragged K (16 blocks)
+    # M=1, 80..127 K blocks: x in LDS, 8 wavefronts
+    (1, 1024, 5120, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
     # M<=4, default (short K, or M > 1)
-    (1, 512, 1024, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    (1, 512, 2048, "gemv 1x1 strips, 16 waves", 16, 16, 1),
     # M 5..16, >=2048 strips
     (8, 32768, 128, "gemv 1x4 strips, 4 waves", 16, 64, 1),
     # M 5..16, >=1024 strips: two strips per 8-wave workgroup
