@@ -72,7 +72,8 @@ class WallTree(torch.nn.Module):
     """A small stand-in with Wall-OSS-style names: an embedding, biased
     attention projections, an MoE-style expert MLP and norms."""
 
-    def __init__(self, vocab: int = 256, hidden: int = 64, inter: int = 192, odd_k: bool = False):
+    def __init__(self, vocab: int = 256, hidden: int = 64, inter: int = 192, odd_k: bool = False,
+                 tied_head: bool = False):
         super().__init__()
         nn = torch.nn
         self.embed_tokens = nn.Embedding(vocab, hidden)
@@ -87,7 +88,11 @@ class WallTree(torch.nn.Module):
             blk.mlp.down_proj = nn.Linear(inter, hidden, bias=False)
             blk.norm = nn.LayerNorm(hidden)
             self.layers.append(blk)
-        self.head = nn.Linear(30 if odd_k else hidden, 48, bias=True)
+        if tied_head:   # an output head sharing the embedding table
+            self.head = nn.Linear(hidden, vocab, bias=False)
+            self.head.weight = self.embed_tokens.weight
+        else:
+            self.head = nn.Linear(30 if odd_k else hidden, 48, bias=True)
 
     def forward(self, ids):
         h = self.embed_tokens(ids)
@@ -104,8 +109,13 @@ def write_tree(path: Path, model: torch.nn.Module, config: dict) -> None:
     from safetensors.torch import save_file
     import json
     path.mkdir(parents=True, exist_ok=True)
-    save_file({k: v.detach().contiguous() for k, v in model.state_dict().items()},
-              str(path / "model.safetensors"))
+    sd, seen = {}, set()
+    for k, v in model.state_dict(keep_vars=True).items():
+        if id(v) in seen:
+            continue  # a tied tensor is stored once, under its first name
+        seen.add(id(v))
+        sd[k] = v.detach().contiguous()
+    save_file(sd, str(path / "model.safetensors"))
     (path / "config.json").write_text(json.dumps(config))
 
 

@@ -303,3 +303,18 @@ def test_wall_oss_list_must_match_the_model(wall, tmp_path):
                                          quantized_weight_count=r["quantized_weight_count"] - 1))
     with pytest.raises(KeyError, match="does not list"):
         load.load_rpu_quant_checkpoint(_skeleton(WallTree), ck3, device="cpu")
+
+
+def test_tied_head_is_loaded_once_and_stays_tied(tmp_path):
+    """A head sharing the embedding table: the checkpoint holds the table once
+    (embed_tokens.weight, kept floating by the default skip list) and the
+    loaded model keeps one tensor under both names."""
+    write_wall_source(tmp_path / "src", seed=9, tied_head=True)
+    convert.convert_wall_oss_checkpoint(tmp_path / "src", tmp_path / "w8", **QUIET)
+    ck = read_all(tmp_path / "w8")
+    assert "head.weight" not in ck
+    model = _skeleton(WallTree, tied_head=True)
+    swapped = load.load_rpu_quant_checkpoint(model, tmp_path / "w8", device="cpu")
+    assert len(swapped) == 8
+    assert model.head.weight is model.embed_tokens.weight
+    assert torch.equal(model.head.weight, ck["embed_tokens.weight"])
