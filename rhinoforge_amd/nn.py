@@ -68,7 +68,7 @@ class W8A16Linear(_LogicalWeightStateDict, nn.Module):
                  device=None) -> None:
         super().__init__()
         if in_features < 8 or in_features % 8:
-            raise ValueError(f"in_features={in_features} must be a positive multiple of 8")
+            raise ValueError(f"in_features={in_features}: the kernels need K > 0 and K % 8 == 0")
         if out_features < 1:
             raise ValueError(f"out_features={out_features} must be >= 1")
         self.in_features = in_features
@@ -153,9 +153,9 @@ class W4A16Linear(_LogicalWeightStateDict, nn.Module):
                  bias: bool = False, device=None) -> None:
         super().__init__()
         if in_features < 64 or in_features % 64:
-            raise ValueError(f"in_features={in_features} must be a positive multiple of 64")
+            raise ValueError(f"in_features={in_features}: int4 tiles need K > 0 and K % 64 == 0")
         if out_features < 16 or out_features % 16:
-            raise ValueError(f"out_features={out_features} must be a positive multiple of 16")
+            raise ValueError(f"out_features={out_features}: int4 tiles need N > 0 and N % 16 == 0")
         if group_size not in (None, 32, 64, 128) or (group_size and in_features % group_size):
             raise ValueError(f"group_size={group_size} must be None (per-channel) or 32/64/128 "
                              f"dividing in_features={in_features}")
