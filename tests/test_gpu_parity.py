@@ -835,3 +835,43 @@ def test_capi_direct_call():
                                sd.data_ptr(), None, y.data_ptr(), 1024, 3, 1024, 4096,
                                capi.KERNEL_GEMV, None, 0, ctypes.c_void_p(stream)) in (
         capi.EWORKSPACE, capi.OK)
+
+
+# ---------------------------------------------------------------- seeded random shapes
+def _random_launches(seed=2026, count=48):
+    """Shapes drawn around the planners' boundaries: M on both sides of
+    16 / 32 / 64 / 128 / 256, 1..4 projections sharing x, N multiples of 16
+    or ragged, K multiples of 64 or a K tail, forced GEMV / GEMM or AUTO."""
+    rng = np.random.default_rng(seed)
+    ms = [1, 2, 3, 4, 5, 8, 15, 16, 17, 24, 31, 32, 33, 48, 63, 64, 65, 96, 127, 128, 129,
+          200, 255, 256, 300, 513]
+    out = []
+    for i in range(count):
+        m = int(rng.choice(ms))
+        ns = [int(rng.integers(1, 64)) * 16 + (int(rng.integers(1, 16)) if rng.random() < 0.3 else 0)
+              for _ in range(int(rng.integers(1, 5)))]
+        k = int(rng.integers(1, 97)) * 64 + (int(rng.integers(1, 8)) * 8 if rng.random() < 0.3 else 0)
+        kernel = str(rng.choice(["auto", "gemv", "gemm"] if m <= 64 else ["auto", "gemm"]))
+        out.append((i, m, ns, k, kernel))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_launches(), ids=lambda c: f"r{c[0]}-{c[1]}x{c[2]}x{c[3]}-{c[4]}")
+def test_random_launch_shapes(case):
+    """linear_multi over seeded random shapes: every projection within the bar
+    (the fp64 oracle on at most 64 rows: the first and last 32)."""
+    i, m, ns, k, kernel = case
+    _say(f"random launch {i}: M={m} N={ns} K={k} kernel={kernel}")
+    x = o.make_activation(o.derive_seed(77, "x", i, m, k), m, k)
+    qs = [o.quantize_linear_per_channel(o.make_weight(o.derive_seed(77, "w", i, j, n, k), n, k))
+          for j, n in enumerate(ns)]
+    bs = [(o.normal(o.derive_seed(77, "b", i, j), (n,)) * 0.1).astype(np.float16) if j % 2 else None
+          for j, n in enumerate(ns)]
+    ys = rf.linear_multi(_to_dev(x), [rf.pack_weight(_to_dev(q)) for q, _ in qs],
+                         [_to_dev(s) for _, s in qs], [None if b is None else _to_dev(b) for b in bs],
+                         kernel=KERNELS[kernel])
+    torch.cuda.synchronize()
+    rows = None if m <= 64 else np.r_[0:32, m - 32:m]
+    for j, ((q, s), b, y) in enumerate(zip(qs, bs, ys)):
+        assert tuple(y.shape) == (m, ns[j])
+        assert_parity(y.cpu().numpy(), x, q, s, b, rows=rows, label=f"proj {j} N={ns[j]}")
