@@ -162,6 +162,27 @@ def test_cfg4_qwen3_vl_32b_projections(m):
         assert_parity(run_gpu(x, q, s, b), x, q, s, b, label=f"cfg4 M={m} {proj}")
 
 
+@pytest.mark.parametrize("m", [1, 32, 512])
+def test_cfg4_fused_launches_as_benched(m):
+    """The fused Qwen3-VL-32B launches the bench times: q/k/v in one
+    linear_multi launch and gate/up in one (at M = 32 the latter runs the
+    32x256 tile across both projections); every row of every output against
+    the CPU path and the fp64 oracle."""
+    x = o.make_activation(o.derive_seed(4, "fused", m), m, 5120, outlier_frac=0.01)
+    xd = _to_dev(x)
+    for group in (("q", "k", "v"), ("gate", "up")):
+        ws = [make_weights(*QWEN3_VL_32B[p], seed=40 + i) for i, p in enumerate(group)]
+        # make_weights keeps one large weight resident: copy the small ones out
+        ws = [(q.copy(), s.copy()) for q, s in ws]
+        _say(f"cfg4 fused {'/'.join(group)} M={m}: "
+             f"{capi.plan(m, [QWEN3_VL_32B[p][0] for p in group], 5120)['name']}")
+        ys = rf.linear_multi(xd, [rf.pack_weight(_to_dev(q)) for q, _ in ws],
+                             [_to_dev(s) for _, s in ws])
+        torch.cuda.synchronize()
+        for p, (q, s), y in zip(group, ws, ys):
+            assert_parity(y.cpu().numpy(), x, q, s, None, label=f"cfg4 fused M={m} {p}")
+
+
 def test_cfg3_qwen3_8b_prefill_mlp():
     """Each MLP projection alone, every row against the CPU path and the fp64 oracle."""
     m = 2048
