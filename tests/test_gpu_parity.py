@@ -649,12 +649,13 @@ def test_op_errors_on_device():
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 1024, 8192), (1, 4096, 1024), (300, 384, 1024),
-                                   (48, 5120, 8192)])
+                                   (48, 5120, 8192), (32, 8192, 5120), (32, 25600, 320)])
 def test_graph_capture_replays_match_eager(m, n, k):
     """The op inside a HIP graph: every replay (with eager work between replays)
     equals the eager result bit for bit.  (16, 1024, 8192) takes the split-K
-    GEMV path and (48, 5120, 8192) the 8-way split mid-M GEMM, whose counters
-    must be left zeroed for the next replay."""
+    GEMV path, (48, 5120, 8192) the 8-way split mid-M GEMM and (32, 8192, 5120)
+    the 4-way split 32x64 tile, whose counters must be left zeroed for the next
+    replay; (32, 25600, 320) the unsplit 32x128 tile."""
     _say(f"graph capture M={m} N={n} K={k}")
     x, q, s, b = make_case(m, n, k, seed=17, bias=True)
     xd, packed, sd, bd = _to_dev(x), rf.pack_weight(_to_dev(q)), _to_dev(s), _to_dev(b)
