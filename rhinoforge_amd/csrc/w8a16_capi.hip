@@ -327,7 +327,8 @@ int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_
   memset(out, 0, sizeof(*out));
   out->kernel = kernel;
   if (kernel == RF_W8A16_KERNEL_GEMV) {
-    const rf::GemvPlan p = int4 ? rf::plan_gemv_int4((int)M, n32[0], (int)K, dev)
+    const rf::GemvPlan p = int4 ? rf::plan_gemv_int4((int)M, n32[0], (int)K,
+                                                     format == RF_W8A16_FORMAT_INT4_GROUP, dev)
                                 : rf::plan_gemv((int)M, n32, count, (int)K, dev);
     int waves = 0;
     bool xl = false;
@@ -563,9 +564,12 @@ size_t rf_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   const int n32 = (int)N;
   size_t extra = rf::gemm_workspace_bytes(rf::plan_gemm((int)M, &n32, 1, (int)K, dev, true));
   if (M <= 64) {
-    const rf::GemvPlan p = rf::plan_gemv_int4((int)M, n32, (int)K, dev);
-    const size_t g = rf::gemv_workspace_bytes(p, (int)M, &n32, 1);
-    extra = g > extra ? g : extra;
+    // Either scale format: the plans may differ.
+    for (const bool grouped : {false, true}) {
+      const rf::GemvPlan p = rf::plan_gemv_int4((int)M, n32, (int)K, grouped, dev);
+      const size_t g = rf::gemv_workspace_bytes(p, (int)M, &n32, 1);
+      extra = g > extra ? g : extra;
+    }
   }
   return RF_W8A16_WS_COUNTER_BYTES + extra;
 }
@@ -621,7 +625,7 @@ int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void
   };
   hipError_t e;
   if (kernel == RF_W8A16_KERNEL_GEMV) {
-    const rf::GemvPlan p = rf::plan_gemv_int4(pr.M, n32, pr.K, dev);
+    const rf::GemvPlan p = rf::plan_gemv_int4(pr.M, n32, pr.K, group_size != 0, dev);
     if (p.splits > 1 && !workspace_ok(rf::gemv_workspace_bytes(p, pr.M, &n32, 1)))
       return RF_W8A16_EWORKSPACE;
     e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);

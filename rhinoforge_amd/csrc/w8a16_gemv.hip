@@ -802,12 +802,25 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
 size_t argmax_slot_bytes(const GemvPlan& p, int M) { return (size_t)M * (size_t)p.groups * 8; }
 
 // Int4 launches: the int8 rules over K counted in 128-wide tiles (one 1 KB
-// tile per 128 positions), with two changes measured on the cfg1 shapes
-// (MI355X): at M 3..4 with many strips the activations are staged in LDS
-// (an int4 tile reads four activation chunks per weight load, so the LDS
-// copy pays off beyond M = 2), and at M 5..16 a long K with few strips
-// takes two strips per workgroup and a 2-way K split.
-GemvPlan plan_gemv_int4(int M, int N, int K, const DeviceInfo& dev) {
+// tile per 128 positions), with these changes, measured on MI355X (cfg1 and
+// Qwen3-VL-32B shapes, N 1024..12288, K 1024..12288, per-channel and
+// group-wise scales, graph-timed):
+//   * M <= 4 on fewer than 257 strips (N <= 4096), where the int8 rules give
+//     one strip per workgroup: an int4 tile reads two activation chunks per
+//     wavefront load for every 128 positions, so staging x in LDS pays off
+//     from a shorter K than for int8 (K >= 2176 per-channel; from K 8192 at
+//     M <= 3 group-wise, whose scale loads share the load queue), and the
+//     16-wavefront staging instance beats the 8-wavefront one from K 8192
+//     (M = 1, 4096 x 12288: 7.10 against 7.64 us; M = 2: 7.38 against
+//     8.83 us); K <= 1024 keeps the 4-wavefront instance per-channel only
+//     (group-wise it loses 5..20%), and 1024 < K <= 2048 keeps 16 wavefronts
+//     of one tile each;
+//   * M 3..4 with many strips: x staged in LDS (an int4 tile reads four
+//     activation chunks per weight load, so the LDS copy pays off beyond
+//     M = 2);
+//   * M 5..16, a long K with few strips: two strips per workgroup and a
+//     2-way K split.
+GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev) {
   const int keff = (int)(round_up(K, kTileK4) / 2);
   GemvPlan p = plan_gemv(M, &N, 1, keff, dev);
   const int ktiles = (int)ceil_div(K, kTileK4);
@@ -815,7 +828,19 @@ GemvPlan plan_gemv_int4(int M, int N, int K, const DeviceInfo& dev) {
   const int cu = dev.cus > 0 ? dev.cus : 256;
   auto fits_xl = [&](int w) { return gemv_lds_bytes(1, 1, w, true, M, ktiles, kTileK4) <= 65536; };
   int cfg = p.cfg, splits = p.splits;
-  if (M >= 3 && M <= 4 && cfg == kG1x2W8U2 && fits_xl(8)) {
+  if (M <= 4 && p.splits == 1 && (int64_t)nstrips * 256 < 257LL * cu && ktiles < 128) {
+    // Below 64 tiles the x copy (at most 4 rows of 63 * 256 bytes) fits.
+    if (ktiles <= 8) {
+      cfg = grouped ? kG1x1W16U2 : kG1x1W4U4;
+    } else if (ktiles <= 16) {
+      cfg = !grouped && M == 1 ? kG1x1W8U4XL : kG1x1W16U2;
+    } else if (ktiles < 64) {
+      if (!grouped) cfg = kG1x1W8U4XL;
+      else cfg = M == 1 || (M == 2 && ktiles >= 40) ? kG1x1W16U4XL : kG1x1W16U2;
+    } else if (M <= 3) {
+      cfg = fits_xl(16) ? kG1x1W16U4XL : kG1x1W16U2;
+    }
+  } else if (M >= 3 && M <= 4 && cfg == kG1x2W8U2 && fits_xl(8)) {
     cfg = kG1x1W8U4XL;
   } else if (M >= 5 && M <= 16 && cfg == kG1x1W16U2 && ktiles >= 64 &&
              (int64_t)nstrips * 256 <= 511LL * cu) {

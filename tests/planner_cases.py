@@ -71,6 +71,37 @@ GEMV_POLICY = [
     (64, 1000, 640, "gemv 4x2 strips, 8 waves", 64, 32, 2),
 ]
 
+# GEMV of packed int4 (forced), per-channel and group-wise scales: the rules
+# that differ from int8 (K counted in 128-wide int4 tiles).  Rows are
+# (M, N, K, group-wise, name, tile_m, tile_n, K splits); packed int4 needs
+# N % 16 == 0 and K % 64 == 0.
+GEMV_INT4_POLICY = [
+    # M <= 4, < 257 strips, <= 8 tiles: four wavefronts per-channel, 16 group-wise
+    (1, 3072, 1024, False, "gemv 1x1 strips, 4 waves", 16, 16, 1),
+    (2, 3072, 1024, True, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # 9..16 tiles: x in LDS per-channel at M = 1, else 16 wavefronts
+    (1, 2048, 2048, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    (2, 2048, 2048, False, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    (1, 2048, 2048, True, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # 17..63 tiles per-channel: x in LDS, 8 wavefronts, up to M = 4 (63 tiles)
+    (4, 1008, 8064, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    (1, 1008, 4160, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),  # K % 128 = 64
+    # 17..63 tiles group-wise: x in LDS at M = 1, and at M = 2 from 40 tiles
+    (1, 1008, 4160, True, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    (2, 1024, 5120, True, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    (2, 1024, 4096, True, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # 64..127 tiles, M <= 3: x in LDS, 16 wavefronts, where the copy fits
+    (2, 4096, 12288, False, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    (2, 1008, 16256, True, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    (3, 4096, 12288, True, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # M = 4 from 64 tiles: the int8 rule
+    (4, 4096, 8192, False, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # M 3..4, >= 640 strips: x in LDS (int8 takes two strips per workgroup)
+    (4, 12288, 4096, True, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # M 5..16, >= 64 tiles on < 512 strips: two strips per workgroup, 2-way K split
+    (16, 4096, 12288, True, "gemv 1x2 strips, 8 waves", 16, 32, 2),
+]
+
 # GEMM (forced).
 GEMM_POLICY = [
     # M < 128: 64x256 tiles

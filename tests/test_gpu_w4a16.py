@@ -15,6 +15,7 @@ import rhinoforge_amd as rf
 from rhinoforge_amd import capi
 from oracle import w4a16 as o4
 from oracle import w8a16 as o8
+import planner_cases
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -102,6 +103,13 @@ CASES = [
     # an int4 tile), per-channel and group-wise
     (500, 5008, 8192, 0), (500, 5008, 8192, 32),
 ]
+
+
+# One shape per int4 GEMV planner rule (planner_cases.GEMV_INT4_POLICY, whose
+# plans the CPU suite checks), group-wise rows with 128-wide groups where K
+# allows, else 32.
+CASES += [(r[0], r[1], r[2], (128 if r[2] % 128 == 0 else 32) if r[3] else 0)
+          for r in planner_cases.GEMV_INT4_POLICY]
 
 
 @pytest.mark.parametrize("m,n,k,gs", CASES)

@@ -11,7 +11,7 @@ from __future__ import annotations
 import pytest
 
 from rhinoforge_amd import capi
-from planner_cases import GEMM_POLICY, GEMV_POLICY
+from planner_cases import GEMM_POLICY, GEMV_INT4_POLICY, GEMV_POLICY
 
 CUS = 256  # MI355X
 
@@ -20,6 +20,16 @@ CUS = 256  # MI355X
 def test_gemv_rule(row):
     m, n, k, name, tm, tn, splits = row
     p = capi.plan(m, n, k, kernel=capi.KERNEL_GEMV, cus=CUS)
+    assert (p["name"], p["tile_m"], p["tile_n"], p["splits"]) == (name, tm, tn, splits), p
+    assert (p["workspace_bytes"] > 0) == (splits > 1)
+
+
+@pytest.mark.parametrize("row", GEMV_INT4_POLICY,
+                         ids=lambda r: f"{r[0]}x{r[1]}x{r[2]}{'g' if r[3] else ''}")
+def test_gemv_int4_rule(row):
+    m, n, k, grouped, name, tm, tn, splits = row
+    fmt = capi.FORMAT_INT4_GROUP if grouped else capi.FORMAT_INT4
+    p = capi.plan(m, n, k, kernel=capi.KERNEL_GEMV, fmt=fmt, cus=CUS)
     assert (p["name"], p["tile_m"], p["tile_n"], p["splits"]) == (name, tm, tn, splits), p
     assert (p["workspace_bytes"] > 0) == (splits > 1)
 
