@@ -803,7 +803,7 @@ size_t argmax_slot_bytes(const GemvPlan& p, int M) { return (size_t)M * (size_t)
 
 // Int4 launches: the int8 rules over K counted in 128-wide tiles (one 1 KB
 // tile per 128 positions), with these changes, measured on MI355X (cfg1 and
-// Qwen3-VL-32B shapes, N 1024..12288, K 1024..12288, per-channel and
+// Qwen3-VL-32B shapes, N 1024..25600, K 1024..25600, per-channel and
 // group-wise scales, graph-timed):
 //   * M <= 4 on fewer than 257 strips (N <= 4096), where the int8 rules give
 //     one strip per workgroup: an int4 tile reads two activation chunks per
@@ -815,20 +815,35 @@ size_t argmax_slot_bytes(const GemvPlan& p, int M) { return (size_t)M * (size_t)
 //     8.83 us); K <= 1024 keeps the 4-wavefront instance per-channel only
 //     (group-wise it loses 5..20%), and 1024 < K <= 2048 keeps 16 wavefronts
 //     of one tile each;
+//   * M <= 4 on 257..639 strips with K >= 8192: x in LDS at M = 1 (and at
+//     M = 2 per-channel) where it fits, else two strips per 16-wavefront
+//     workgroup (int4's x copy is twice int8's per weight byte and stops
+//     fitting in LDS at M = 2 from K 16384; VL-32B down 5120 x 25600 at
+//     M = 2: 22.1 against 28.4 us);
 //   * M 3..4 with many strips: x staged in LDS (an int4 tile reads four
 //     activation chunks per weight load, so the LDS copy pays off beyond
 //     M = 2);
-//   * M 5..16, a long K with few strips: two strips per workgroup and a
-//     2-way K split.
+//   * M 8..16 on >= 1536 strips: four strips per 4-wavefront workgroup
+//     (int8 takes two below 2048 strips; 25600 x 5120 at M = 16: 20.5
+//     against 26.8 us; at 1024..1280 strips, or at M = 5, it loses up to
+//     20%);
+//   * M 5..16 on 257..511 strips: from K 16384 four strips per workgroup
+//     with a 2-way K split (5120 x 25600 at M = 16: 25.9 against 34.4 us),
+//     and at M >= 8 from K 8192 two strips per 8-wavefront workgroup;
+//   * M 5..16, a long K with fewer strips: two strips per workgroup and a
+//     2-way K split;
+//   * M 5..8 on <= 64 strips: no K split (1024 x 4096 at M = 8: 5.1
+//     against 5.8 us).
 GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev) {
   const int keff = (int)(round_up(K, kTileK4) / 2);
   GemvPlan p = plan_gemv(M, &N, 1, keff, dev);
   const int ktiles = (int)ceil_div(K, kTileK4);
   const int nstrips = (int)ceil_div(N, 16);
   const int cu = dev.cus > 0 ? dev.cus : 256;
+  auto strips_ge = [&](int n256) { return (int64_t)nstrips * 256 >= (int64_t)n256 * cu; };
   auto fits_xl = [&](int w) { return gemv_lds_bytes(1, 1, w, true, M, ktiles, kTileK4) <= 65536; };
   int cfg = p.cfg, splits = p.splits;
-  if (M <= 4 && p.splits == 1 && (int64_t)nstrips * 256 < 257LL * cu && ktiles < 128) {
+  if (M <= 4 && p.splits == 1 && !strips_ge(257) && ktiles < 128) {
     // Below 64 tiles the x copy (at most 4 rows of 63 * 256 bytes) fits.
     if (ktiles <= 8) {
       cfg = grouped ? kG1x1W16U2 : kG1x1W4U4;
@@ -840,14 +855,30 @@ GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev
     } else if (M <= 3) {
       cfg = fits_xl(16) ? kG1x1W16U4XL : kG1x1W16U2;
     }
+  } else if (M <= 4 && p.splits == 1 && strips_ge(257) && !strips_ge(640) && ktiles >= 64) {
+    cfg = (M == 1 || (M == 2 && !grouped)) && fits_xl(8) ? kG1x1W8U4XL : kG1x2W16U2;
   } else if (M >= 3 && M <= 4 && cfg == kG1x2W8U2 && fits_xl(8)) {
     cfg = kG1x1W8U4XL;
+  } else if (M >= 8 && M <= 16 && strips_ge(1536)) {
+    cfg = kG1x4W4U2;
+  } else if (M >= 5 && M <= 16 && cfg == kG1x2W16U2 && p.splits == 1 &&
+             (ktiles >= 128 || (M >= 8 && ktiles >= 64))) {
+    // (257..511 strips)
+    if (ktiles >= 128) {
+      cfg = kG1x4W8U2;
+      splits = 2;
+    } else {
+      cfg = kG1x2W8U2;
+    }
   } else if (M >= 5 && M <= 16 && cfg == kG1x1W16U2 && ktiles >= 64 &&
              (int64_t)nstrips * 256 <= 511LL * cu) {
     cfg = kG1x2W8U2;
     splits = 2;
+  } else if (M >= 5 && M <= 8 && cfg == kG1x2W16U2 && p.splits > 1 && !strips_ge(65)) {
+    cfg = kG1x1W16U2;
+    splits = 1;
   }
-  if (cfg == p.cfg) return p;
+  if (cfg == p.cfg && splits == p.splits) return p;
   GemvPlan q;
   q.cfg = cfg;
   q.mt = kGemvCfgs[cfg].mt;

@@ -96,10 +96,27 @@ GEMV_INT4_POLICY = [
     (3, 4096, 12288, True, "gemv 1x1 strips, 16 waves", 16, 16, 1),
     # M = 4 from 64 tiles: the int8 rule
     (4, 4096, 8192, False, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # M <= 4, 257..639 strips, >= 64 tiles: x in LDS at M = 1 and at M = 2
+    # per-channel where it fits, else two strips per 16-wave workgroup
+    (1, 5120, 8192, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    (2, 6144, 12288, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    (2, 6144, 12288, True, "gemv 1x2 strips, 16 waves", 16, 32, 1),
+    (2, 5120, 25600, False, "gemv 1x2 strips, 16 waves", 16, 32, 1),
     # M 3..4, >= 640 strips: x in LDS (int8 takes two strips per workgroup)
     (4, 12288, 4096, True, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
-    # M 5..16, >= 64 tiles on < 512 strips: two strips per workgroup, 2-way K split
+    # M 8..16, >= 1536 strips: four strips per 4-wave workgroup; M 5 keeps two
+    (8, 25600, 5120, False, "gemv 1x4 strips, 4 waves", 16, 64, 1),
+    (5, 25600, 5120, False, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 5..16, 257..511 strips, >= 128 tiles: four strips, 2-way K split
+    (5, 5120, 25600, True, "gemv 1x4 strips, 8 waves", 16, 64, 2),
+    # the same strips at 64..127 tiles: two strips per 8-wave workgroup from M 8
+    (8, 5120, 8192, True, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    (5, 5120, 8192, True, "gemv 1x2 strips, 16 waves", 16, 32, 1),
+    # M 5..16, >= 64 tiles on < 257 strips: two strips per workgroup, 2-way K split
     (16, 4096, 12288, True, "gemv 1x2 strips, 8 waves", 16, 32, 2),
+    # M 5..8, <= 64 strips: no K split (int8 splits 4 ways); from M 9 the split
+    (8, 1024, 4096, False, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    (12, 1024, 4096, False, "gemv 1x2 strips, 16 waves", 16, 32, 4),
 ]
 
 # GEMM (forced).
