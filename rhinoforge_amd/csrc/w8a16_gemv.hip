@@ -679,6 +679,13 @@ enum GemvCfgId {
   kG2x1W8U4,     // MT=2 NS=1 W=8  U=4
   kG4x2W8U1,     // MT=4 NS=2 W=8  U=1
   kG4x2W4U1,     // MT=4 NS=2 W=4  U=1
+  // Launches of many strips at M 5..16 (int8): as many strips per workgroup
+  // as give about one workgroup per CU (or two, NS=3), so the activation
+  // fragment each wavefront loads serves 3..7 weight tiles.
+  kG1x3W8U2,     // MT=1 NS=3 W=8  U=2
+  kG1x5W8U1,     // MT=1 NS=5 W=8  U=1
+  kG1x6W8U1,     // MT=1 NS=6 W=8  U=1
+  kG1x7W8U1,     // MT=1 NS=7 W=8  U=1
   kGemvCfgCount
 };
 
@@ -691,6 +698,7 @@ constexpr GemvCfgDesc kGemvCfgs[kGemvCfgCount] = {
     {1, 1, 16, false}, {1, 1, 16, true}, {1, 1, 8, false}, {1, 1, 8, true}, {1, 1, 4, false},
     {1, 2, 16, false}, {1, 4, 8, false}, {1, 4, 4, false}, {1, 2, 8, false},
     {2, 4, 4, false},  {2, 2, 8, false}, {2, 1, 8, false}, {4, 2, 8, false}, {4, 2, 4, false},
+    {1, 3, 8, false},  {1, 5, 8, false}, {1, 6, 8, false}, {1, 7, 8, false},
 };
 
 bool lds_fits(int cfg, int M, int kb_per_split) {
@@ -714,6 +722,10 @@ hipError_t launch_gemv_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStrea
     case kG2x1W8U4: return launch_t<2, 1, 8, 4, false, true>(ka, p, stream);
     case kG4x2W8U1: return launch_t<4, 2, 8, 1, false, true>(ka, p, stream);
     case kG4x2W4U1: return launch_t<4, 2, 4, 1, false, true>(ka, p, stream);
+    case kG1x3W8U2: return launch_t<1, 3, 8, 2, false, true>(ka, p, stream);
+    case kG1x5W8U1: return launch_t<1, 5, 8, 1, false, true>(ka, p, stream);
+    case kG1x6W8U1: return launch_t<1, 6, 8, 1, false, true>(ka, p, stream);
+    case kG1x7W8U1: return launch_t<1, 7, 8, 1, false, true>(ka, p, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -756,7 +768,7 @@ hipError_t launch_gemv4_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStre
     case kG2x1W8U4: return launch_t<2, 1, 8, 2, false, true, WF>(ka, p, stream);
     case kG4x2W8U1: return launch_t<4, 2, 8, 1, false, true, WF>(ka, p, stream);
     case kG4x2W4U1: return launch_t<4, 2, 4, 1, false, true, WF>(ka, p, stream);
-    default: return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;  // (the one-round int8 configurations: not planned)
   }
 }
 
@@ -801,6 +813,9 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
 
 size_t argmax_slot_bytes(const GemvPlan& p, int M) { return (size_t)M * (size_t)p.groups * 8; }
 
+GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
+                         bool one_round);
+
 // Int4 launches: the int8 rules over K counted in 128-wide tiles (one 1 KB
 // tile per 128 positions), with these changes, measured on MI355X (cfg1 and
 // Qwen3-VL-32B shapes, N 1024..25600, K 1024..25600, per-channel and
@@ -836,7 +851,7 @@ size_t argmax_slot_bytes(const GemvPlan& p, int M) { return (size_t)M * (size_t)
 //     against 5.8 us).
 GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev) {
   const int keff = (int)(round_up(K, kTileK4) / 2);
-  GemvPlan p = plan_gemv(M, &N, 1, keff, dev);
+  GemvPlan p = plan_gemv_rules(M, &N, 1, keff, dev, false);
   const int ktiles = (int)ceil_div(K, kTileK4);
   const int nstrips = (int)ceil_div(N, 16);
   const int cu = dev.cus > 0 ? dev.cus : 256;
@@ -901,7 +916,11 @@ GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev
 //     strips share it when there are enough strips to fill the chip;
 //   * M 17..64: two / four 16-row m-tiles per wavefront;
 //   * K splits only where the strips alone cannot fill 256 CUs.
-GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev) {
+// one_round: the int8 rules at M 5..16 that give a workgroup three to seven
+// strips (kG1x3W8U2 .. kG1x7W8U1, sized to about one or two workgroups per
+// CU); the int4 planner starts from the rules without them.
+GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
+                         bool one_round) {
   // Rules see the launch's strips of all projections together.
   int nstrips = 0;
   for (int i = 0; i < nproj; ++i) nstrips += (int)ceil_div(Ns[i], 16);
@@ -943,8 +962,23 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
                                                                              : kG1x1W16U2;
     }
   } else if (M <= 16) {
+    // Strips per CU, rounded up (one-round rules below).
+    const int64_t spc = ((int64_t)nstrips + cu - 1) / cu;
     if (strips_ge(2048)) {
-      cfg = kG1x4W4U2;
+      // M 5..8 (rows 8..15 of the activation fragment repeat row M-1, so
+      // it costs less): three strips per workgroup (Qwen3-14B lm_head
+      // 151936 x 5120 at M 8: 117.9 instead of 119.6 us; 32768 x 4096:
+      // 23.3 instead of 25.1 us).
+      cfg = (one_round && M <= 8) ? kG1x3W8U2 : kG1x4W4U2;
+    } else if (one_round && strips_ge(1025) && spc <= 7) {
+      // 5..7 strips per CU: that many strips per 8-wave workgroup, one
+      // workgroup per CU, so each activation fragment serves 5..7 weight
+      // tiles; at 6 per CU and M <= 12 three strips, two workgroups per CU
+      // (MI355X, four rotated weight copies: Qwen3-8B fused gate/up
+      // 24576 x 4096 at M 16: 18.8 instead of 21.6 us, at M 5..12 17.7..18.0
+      // instead of 18.9..20.6 us; 20480 x 4096 at M 16: 16.1 instead of
+      // 20.2 us; 28672 x 4096: 21.7 instead of 25.9 us).
+      cfg = spc == 5 ? kG1x5W8U1 : spc == 7 ? kG1x7W8U1 : M <= 12 ? kG1x3W8U2 : kG1x6W8U1;
     } else if (strips_ge(1024)) {
       cfg = kG1x2W8U2;
     } else if (strips_ge(640)) {
@@ -993,6 +1027,10 @@ GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   p.kb_per_split = (int)ceil_div(kblocks, splits);
   p.splits = (int)ceil_div(kblocks, p.kb_per_split);  // drop empty splits
   return p;
+}
+
+GemvPlan plan_gemv(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev) {
+  return plan_gemv_rules(M, Ns, nproj, K, dev, true);
 }
 
 }  // namespace rf

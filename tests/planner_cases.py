@@ -34,8 +34,21 @@ GEMV_POLICY = [
     (1, 1024, 5120, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
     # M<=4, default (short K, or M > 1)
     (1, 512, 2048, "gemv 1x1 strips, 16 waves", 16, 16, 1),
-    # M 5..16, >=2048 strips
-    (8, 32768, 128, "gemv 1x4 strips, 4 waves", 16, 64, 1),
+    # M 9..16, >=2048 strips
+    (12, 32768, 128, "gemv 1x4 strips, 4 waves", 16, 64, 1),
+    # M 5..8, >=2048 strips: three strips per 8-wave workgroup
+    (8, 32768, 128, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    (5, 40016, 136, "gemv 1x3 strips, 8 waves", 16, 48, 1),    # ragged N (2501 strips), K tail
+    # M 5..16, 1025..1792 strips (5..7 per CU): one workgroup per CU
+    (16, 20480, 256, "gemv 1x5 strips, 8 waves", 16, 80, 1),
+    (16, 24576, 512, "gemv 1x6 strips, 8 waves", 16, 96, 1),
+    (13, 24000, 200, "gemv 1x6 strips, 8 waves", 16, 96, 1),   # ragged N (1500 strips), K tail
+    (16, 28672, 128, "gemv 1x7 strips, 8 waves", 16, 112, 1),
+    (9, 26000, 320, "gemv 1x7 strips, 8 waves", 16, 112, 1),    # 1625 strips
+    # 6 per CU at M <= 12: three strips, two workgroups per CU
+    (12, 24576, 512, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    # M 3..4 at 1536 strips keeps two strips per workgroup
+    (4, 24576, 256, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     # M 5..16, >=1024 strips: two strips per 8-wave workgroup
     (16, 16384, 256, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     # M 5..16, 640..1023 strips: 4 strips per workgroup
