@@ -679,9 +679,9 @@ enum GemvCfgId {
   kG2x1W8U4,     // MT=2 NS=1 W=8  U=4
   kG4x2W8U1,     // MT=4 NS=2 W=8  U=1
   kG4x2W4U1,     // MT=4 NS=2 W=4  U=1
-  // Launches of many strips at M 5..16 (int8): as many strips per workgroup
-  // as give about one workgroup per CU (or two, NS=3), so the activation
-  // fragment each wavefront loads serves 3..7 weight tiles.
+  // Launches of many strips at M 5..16: as many strips per workgroup as give
+  // about one workgroup per CU (or two, NS=3), so the activation fragment
+  // each wavefront loads serves 3..7 weight tiles (int4 at half the unroll).
   kG1x3W8U2,     // MT=1 NS=3 W=8  U=2
   kG1x5W8U1,     // MT=1 NS=5 W=8  U=1
   kG1x6W8U1,     // MT=1 NS=6 W=8  U=1
@@ -768,7 +768,10 @@ hipError_t launch_gemv4_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStre
     case kG2x1W8U4: return launch_t<2, 1, 8, 2, false, true, WF>(ka, p, stream);
     case kG4x2W8U1: return launch_t<4, 2, 8, 1, false, true, WF>(ka, p, stream);
     case kG4x2W4U1: return launch_t<4, 2, 4, 1, false, true, WF>(ka, p, stream);
-    default: return hipErrorInvalidValue;  // (the one-round int8 configurations: not planned)
+    case kG1x3W8U2: return launch_t<1, 3, 8, 1, false, true, WF>(ka, p, stream);
+    case kG1x6W8U1: return launch_t<1, 6, 8, 1, false, true, WF>(ka, p, stream);
+    case kG1x7W8U1: return launch_t<1, 7, 8, 1, false, true, WF>(ka, p, stream);
+    default: return hipErrorInvalidValue;  // (kG1x5W8U1: not planned for int4)
   }
 }
 
@@ -848,7 +851,15 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
 //   * M 5..16, a long K with fewer strips: two strips per workgroup and a
 //     2-way K split;
 //   * M 5..8 on <= 64 strips: no K split (1024 x 4096 at M = 8: 5.1
-//     against 5.8 us).
+//     against 5.8 us);
+//   * M 5..16, about three, six or seven strips per CU (513..768,
+//     1281..1536, 1537..1792 strips, no K split): that many strips per
+//     8-wave workgroup, one workgroup per CU (three strips, two per CU, at
+//     six per CU below M 12), so each activation fragment -- four chunks
+//     per wavefront and tile -- serves 3..7 weight tiles (per-channel and
+//     group-wise alike: 12288 x 4096 at M 5..16 7.3..9.1 against
+//     8.8..9.7 us; 24576 x 4096 at M 16 13.7 against 16.4 us, at M 8 12.3
+//     against 14.1 us; 25600 x 5120 at M 16 19.1 against 20.8 us).
 GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev) {
   const int keff = (int)(round_up(K, kTileK4) / 2);
   GemvPlan p = plan_gemv_rules(M, &N, 1, keff, dev, false);
@@ -858,7 +869,10 @@ GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev
   auto strips_ge = [&](int n256) { return (int64_t)nstrips * 256 >= (int64_t)n256 * cu; };
   auto fits_xl = [&](int w) { return gemv_lds_bytes(1, 1, w, true, M, ktiles, kTileK4) <= 65536; };
   int cfg = p.cfg, splits = p.splits;
-  if (M <= 4 && p.splits == 1 && !strips_ge(257) && ktiles < 128) {
+  const int64_t spc = ((int64_t)nstrips + cu - 1) / cu;  // strips per CU, rounded up
+  if (M >= 5 && M <= 16 && p.splits == 1 && strips_ge(513) && (spc == 3 || spc == 6 || spc == 7)) {
+    cfg = spc == 3 ? kG1x3W8U2 : spc == 7 ? kG1x7W8U1 : M >= 12 ? kG1x6W8U1 : kG1x3W8U2;
+  } else if (M <= 4 && p.splits == 1 && !strips_ge(257) && ktiles < 128) {
     // Below 64 tiles the x copy (at most 4 rows of 63 * 256 bytes) fits.
     if (ktiles <= 8) {
       cfg = grouped ? kG1x1W16U2 : kG1x1W4U4;
@@ -981,10 +995,15 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
       cfg = spc == 5 ? kG1x5W8U1 : spc == 7 ? kG1x7W8U1 : M <= 12 ? kG1x3W8U2 : kG1x6W8U1;
     } else if (strips_ge(1024)) {
       cfg = kG1x2W8U2;
+    } else if (one_round && strips_ge(513) && spc == 3) {
+      // 3 strips per CU: three strips per 8-wave workgroup, one workgroup
+      // per CU (12288 x 4096 at M 5 / 8 / 16: 10.4 / 10.9 / 11.2 instead of
+      // 12.6 / 12.8 / 13.1 us with four strips per workgroup).
+      cfg = kG1x3W8U2;
     } else if (strips_ge(640)) {
       cfg = kG1x4W8U2;
     } else if (strips_ge(512)) {
-      cfg = kG1x2W8U2;  // 512..639 strips: four per workgroup leaves half the CUs idle
+      cfg = kG1x2W8U2;  // 512 strips: four per workgroup leaves half the CUs idle
     } else if (strips_ge(257)) {
       cfg = kG1x2W16U2;
     } else if (kblocks >= 128) {

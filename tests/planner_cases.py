@@ -51,8 +51,11 @@ GEMV_POLICY = [
     (4, 24576, 256, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     # M 5..16, >=1024 strips: two strips per 8-wave workgroup
     (16, 16384, 256, "gemv 1x2 strips, 8 waves", 16, 32, 1),
-    # M 5..16, 640..1023 strips: 4 strips per workgroup
-    (12, 10240, 256, "gemv 1x4 strips, 8 waves", 16, 64, 1),
+    # M 5..16, 769..1023 strips: 4 strips per workgroup
+    (12, 14336, 256, "gemv 1x4 strips, 8 waves", 16, 64, 1),
+    # M 5..16, 513..768 strips: three strips per workgroup
+    (12, 10240, 256, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    (16, 12288, 4096, "gemv 1x3 strips, 8 waves", 16, 48, 1),
     # M 5..16, 257..511 strips: two strips per 16-wave workgroup
     (10, 5000, 512, "gemv 1x2 strips, 16 waves", 16, 32, 1),
     # M 5..16, long K: 4-way K split
@@ -68,7 +71,7 @@ GEMV_POLICY = [
     (1, 8192, 5120, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
     # M 3..4, the same strips and K: 2 strips per workgroup
     (4, 5120, 8192, "gemv 1x2 strips, 8 waves", 16, 32, 1),
-    # M 5..16, 512..639 strips: 2 strips per workgroup
+    # M 5..16, 512 strips (two per CU): 2 strips per workgroup
     (12, 8192, 512, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     # M 17..32, >=1024 strips
     (20, 16384, 128, "gemv 2x4 strips, 4 waves", 32, 64, 1),
@@ -117,9 +120,18 @@ GEMV_INT4_POLICY = [
     (2, 5120, 25600, False, "gemv 1x2 strips, 16 waves", 16, 32, 1),
     # M 3..4, >= 640 strips: x in LDS (int8 takes two strips per workgroup)
     (4, 12288, 4096, True, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
-    # M 8..16, >= 1536 strips: four strips per 4-wave workgroup; M 5 keeps two
-    (8, 25600, 5120, False, "gemv 1x4 strips, 4 waves", 16, 64, 1),
-    (5, 25600, 5120, False, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 8..16, >= 1793 strips: four strips per 4-wave workgroup; M 5..7 at
+    # 1025..1280 strips keeps two
+    (8, 32768, 4096, False, "gemv 1x4 strips, 4 waves", 16, 64, 1),
+    (5, 20480, 4096, False, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 5..16, 3 / 6 / 7 strips per CU: that many strips per 8-wave
+    # workgroup (three at 6 per CU below M 12)
+    (5, 12288, 4096, True, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    (16, 10000, 2048, False, "gemv 1x3 strips, 8 waves", 16, 48, 1),   # 625 strips
+    (16, 24576, 4096, True, "gemv 1x6 strips, 8 waves", 16, 96, 1),
+    (8, 24576, 4096, False, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    (8, 25600, 5120, False, "gemv 1x7 strips, 8 waves", 16, 112, 1),
+    (12, 27008, 4224, True, "gemv 1x7 strips, 8 waves", 16, 112, 1),  # 1688 strips, K % 128 = 0
     # M 5..16, 257..511 strips, >= 128 tiles: four strips, 2-way K split
     (5, 5120, 25600, True, "gemv 1x4 strips, 8 waves", 16, 64, 2),
     # the same strips at 64..127 tiles: two strips per 8-wave workgroup from M 8
