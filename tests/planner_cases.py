@@ -205,3 +205,19 @@ GEMM_POLICY = [
     (64, 1000, 200, "gemm 64x64 4-stage", 64, 64, 1),      # ragged N, 4 K blocks: no split
     (33, 4104, 520, "gemm 64x64 4-stage", 64, 64, 1),      # ragged M and N, K tail (9 K blocks)
 ]
+
+# Launches of several projections sharing x where the GEMV planner gives a
+# workgroup three to seven strips (513..1792 strips at M 5..16, from 2048 at
+# M <= 8): (M, N per projection, K, the plan's name on a 256-CU part).  They
+# mix ragged projections, so a workgroup's strips run past its projection's
+# last strip, and K tails.
+STRIP_GROUP_LAUNCHES = [
+    (16, [4000, 4000, 1032], 1032, "gemv 1x3 strips, 8 waves"),
+    (16, [10000, 10480], 512, "gemv 1x5 strips, 8 waves"),
+    (13, [12000, 12008, 264], 256, "gemv 1x6 strips, 8 waves"),
+    (9, [12000, 12000], 456, "gemv 1x3 strips, 8 waves"),
+    (16, [9000, 9000, 9000], 320, "gemv 1x7 strips, 8 waves"),
+    (6, [20000, 20000, 40], 192, "gemv 1x3 strips, 8 waves"),
+]
+
+

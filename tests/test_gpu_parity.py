@@ -859,6 +859,31 @@ def test_capi_direct_call():
         capi.EWORKSPACE, capi.OK)
 
 
+# ------------------------------------------- several projections, 3..7 strips per workgroup
+@pytest.mark.parametrize("case", planner_cases.STRIP_GROUP_LAUNCHES, ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}")
+def test_linear_multi_strip_groups(case):
+    """linear_multi where the planner gives each workgroup three to seven
+    strips: every row of every projection within the bar, and a second call
+    bit-identical to the first."""
+    m, ns, k, name = case
+    _say(f"strip groups M={m} N={ns} K={k}")
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert capi.plan(m, ns, k)["name"] == name
+    x = o.make_activation(o.derive_seed(91, "x", m, k), m, k)
+    qs = [o.quantize_linear_per_channel(o.make_weight(o.derive_seed(91, "w", j, n, k), n, k))
+          for j, n in enumerate(ns)]
+    bs = [(o.normal(o.derive_seed(91, "b", j, n), (n,)) * 0.1).astype(np.float16) if j == 1 else None
+          for j, n in enumerate(ns)]
+    args = ([rf.pack_weight(_to_dev(q)) for q, _ in qs], [_to_dev(s) for _, s in qs],
+            [None if b is None else _to_dev(b) for b in bs])
+    ys = rf.linear_multi(_to_dev(x), *args)
+    ys2 = rf.linear_multi(_to_dev(x), *args)
+    torch.cuda.synchronize()
+    for j, ((q, s), b, y, y2) in enumerate(zip(qs, bs, ys, ys2)):
+        assert torch.equal(y, y2), f"proj {j}: second call differs"
+        assert_parity(y.cpu().numpy(), x, q, s, b, label=f"proj {j} N={ns[j]}")
+
+
 # ---------------------------------------------------------------- seeded random shapes
 def _random_launches(seed=2026, count=48):
     """Shapes drawn around the planners' boundaries: M on both sides of

@@ -11,7 +11,7 @@ from __future__ import annotations
 import pytest
 
 from rhinoforge_amd import capi
-from planner_cases import GEMM_POLICY, GEMV_INT4_POLICY, GEMV_POLICY
+from planner_cases import GEMM_POLICY, GEMV_INT4_POLICY, GEMV_POLICY, STRIP_GROUP_LAUNCHES
 
 CUS = 256  # MI355X
 
@@ -32,6 +32,13 @@ def test_gemv_int4_rule(row):
     p = capi.plan(m, n, k, kernel=capi.KERNEL_GEMV, fmt=fmt, cus=CUS)
     assert (p["name"], p["tile_m"], p["tile_n"], p["splits"]) == (name, tm, tn, splits), p
     assert (p["workspace_bytes"] > 0) == (splits > 1)
+
+
+@pytest.mark.parametrize("row", STRIP_GROUP_LAUNCHES, ids=lambda r: f"{r[0]}x{r[1]}x{r[2]}")
+def test_gemv_strip_group_launches(row):
+    m, ns, k, name = row
+    p = capi.plan(m, ns, k, cus=CUS)
+    assert (p["kernel"], p["name"], p["splits"]) == ("gemv", name, 1), p
 
 
 @pytest.mark.parametrize("row", GEMM_POLICY, ids=lambda r: f"{r[0]}x{r[1]}x{r[2]}")
