@@ -922,3 +922,48 @@ def test_random_launch_shapes(case):
     for j, ((q, s), b, y) in enumerate(zip(qs, bs, ys)):
         assert tuple(y.shape) == (m, ns[j])
         assert_parity(y.cpu().numpy(), x, q, s, b, rows=rows, label=f"proj {j} N={ns[j]}")
+
+
+def _random_wide_launches(seed=4099, count=24):
+    """Wide launches: 1..4 projections summing to 513..32768 columns (the
+    planners' many-strip rules, three to seven strips per workgroup among
+    them), M 1..64, ragged N and K tails, AUTO or forced GEMV."""
+    rng = np.random.default_rng(seed)
+    ms = [1, 2, 3, 4, 5, 6, 8, 9, 12, 13, 16, 24, 32, 48, 64]
+    out = []
+    for i in range(count):
+        m = int(rng.choice(ms))
+        total = int(rng.integers(513, 2049)) * 16
+        parts = int(rng.integers(1, 5))
+        cuts = np.sort(rng.choice(np.arange(1, total // 16), parts - 1, replace=False)) * 16
+        ns = [int(b - a) for a, b in zip(np.r_[0, cuts], np.r_[cuts, total])]
+        if rng.random() < 0.5:
+            ns[-1] -= int(rng.integers(1, 16))  # a ragged last projection
+        k = int(rng.integers(2, 33)) * 64 + (int(rng.integers(1, 8)) * 8 if rng.random() < 0.3 else 0)
+        kernel = str(rng.choice(["auto", "gemv"]))
+        out.append((i, m, ns, k, kernel))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_wide_launches(),
+                         ids=lambda c: f"w{c[0]}-{c[1]}x{sum(c[2])}x{c[3]}-{c[4]}")
+def test_random_wide_launch_shapes(case):
+    """linear_multi over seeded wide random launches: every projection within
+    the bar on its first and last rows (all rows up to M = 16)."""
+    i, m, ns, k, kernel = case
+    _say(f"wide random launch {i}: M={m} N={ns} K={k} kernel={kernel} "
+         f"plan={capi.plan(m, ns, k, kernel=KERNELS[kernel])['name']}")
+    x = o.make_activation(o.derive_seed(78, "x", i, m, k), m, k)
+    qs = [o.quantize_linear_per_channel(o.make_weight(o.derive_seed(78, "w", i, j, n, k), n, k))
+          for j, n in enumerate(ns)]
+    bs = [(o.normal(o.derive_seed(78, "b", i, j), (n,)) * 0.1).astype(np.float16) if j % 2 else None
+          for j, n in enumerate(ns)]
+    ys = rf.linear_multi(_to_dev(x), [rf.pack_weight(_to_dev(q)) for q, _ in qs],
+                         [_to_dev(s) for _, s in qs], [None if b is None else _to_dev(b) for b in bs],
+                         kernel=KERNELS[kernel])
+    torch.cuda.synchronize()
+    rows = None if m <= 16 else np.r_[0:8, m - 8:m]
+    for j, ((q, s), b, y) in enumerate(zip(qs, bs, ys)):
+        assert tuple(y.shape) == (m, ns[j])
+        assert_parity(y.cpu().numpy(), x, q, s, b, rows=rows, label=f"proj {j} N={ns[j]}")
+

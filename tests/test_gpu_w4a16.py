@@ -244,3 +244,34 @@ def test_w4a16_graph_replays_match_eager(m, n, k, gs):
         assert torch.equal(out, eager), f"replay {i}"
         assert torch.equal(rf.linear_w4a16(xd, wp, sd), eager)
     check(out.cpu().numpy(), x, q, s, label=f"w4 graph {m}x{n}x{k} gs={gs}")
+
+
+def _random_int4_launches(seed=4100, count=24):
+    """Packed int4 over seeded random shapes: M 1..64 (GEMV) and a few GEMM
+    rows, 16..2048 strips, K a multiple of 64 (K % 128 == 64 included),
+    per-channel and group-wise scales."""
+    rng = np.random.default_rng(seed)
+    ms = [1, 2, 3, 4, 5, 8, 9, 12, 16, 24, 32, 48, 64, 96, 200]
+    out = []
+    for i in range(count):
+        m = int(rng.choice(ms))
+        n = int(rng.integers(1, 2049)) * 16
+        k = int(rng.integers(1, 49)) * 64
+        gs = int(rng.choice([0, 32, 64, 128]))
+        if gs and k % gs:
+            gs = 32
+        out.append((i, m, n, k, gs))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_int4_launches(),
+                         ids=lambda c: f"r{c[0]}-{c[1]}x{c[2]}x{c[3]}-g{c[4]}")
+def test_w4a16_random_shapes(case):
+    i, m, n, k, gs = case
+    _say(f"w4a16 random {i}: M={m} N={n} K={k} gs={gs}")
+    q, s = make_w4(n, k, gs, 40 + i)
+    x = o8.make_activation(o8.derive_seed(40, "x4r", i, m, k), m, k)
+    y = run(x, q, s)
+    rows = None if m <= 16 else np.r_[0:8, m - 8:m]
+    check(y, x, q, s, label=f"w4 random {m}x{n}x{k} gs={gs}", rows=rows)
+
