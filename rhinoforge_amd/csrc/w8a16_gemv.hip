@@ -74,6 +74,8 @@ struct GemvKernelArgs {
   // Group-wise int4: log2(group_size / 32); scale row of tile position k is
   // k / group_size.
   int gshift;
+  // Nonzero: groups per XCD run (xcd_group), the launch's groups / 8.
+  int xcd_run;
 };
 
 // Argmax key of output value v at column n: the fp16 value mapped to an
@@ -276,6 +278,19 @@ __device__ __forceinline__ void argmax_store(const GemvKernelArgs& a, const unsi
     a.amax_slots[(int64_t)m * gridDim.x + blockIdx.x] = row_key[m];
 }
 
+// Group (strip range) of workgroup bx out of G.  The hardware deals
+// workgroups to the 8 XCDs round-robin by dispatch id, x fastest, so with
+// group = bx adjacent strips run on different XCDs.  A 128-byte line of a
+// group-wise scale row holds the scales of four adjacent strips (32 bytes
+// each), and every XCD's L2 would fetch it: four times the scale traffic.
+// Here the groups an XCD runs form one contiguous range of `run` = G / 8
+// groups (the first 8 * run workgroups; any rest keep their id), a bijection
+// of [0, G) either way; run = 0 keeps every id.  Branch-free, so the load of
+// `run` joins the kernel's other argument loads.
+__device__ __forceinline__ int xcd_group(int bx, int run) {
+  return bx < 8 * run ? (bx & 7) * run + (bx >> 3) : bx;
+}
+
 // WF (WeightFormat): int8 tiles (64 input positions, two MFMAs per tile and
 // strip) or int4 tiles (128 positions, four MFMAs); group-wise int4 loads one
 // scale per lane, tile and strip alongside the weights and applies it at
@@ -291,13 +306,17 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-  const int group = blockIdx.x;
+  const int group = GS ? xcd_group(blockIdx.x, a.xcd_run) : (int)blockIdx.x;
   const int split = blockIdx.y;
-  // Projection of this workgroup (uniform across it).
+  // Projection of this workgroup (uniform across it).  Group-wise int4
+  // launches carry one projection (launch_gemv refuses more), so their
+  // argument loads need not wait for the remapped group.
   int pi = 0;
+  if (!GS) {
 #pragma unroll
-  for (int i = 1; i < kMaxProj; ++i)
-    if (i < a.nproj && group >= a.proj[i].group0) pi = i;
+    for (int i = 1; i < kMaxProj; ++i)
+      if (i < a.nproj && group >= a.proj[i].group0) pi = i;
+  }
   const uint8_t* const P_w = a.proj[pi].w;
   const _Float16* const P_scale = a.proj[pi].scale;
   const _Float16* const P_bias = a.proj[pi].bias;
@@ -659,6 +678,17 @@ GemvKernelArgs make_args(const LinearProblem& pr, const GemvPlan& p, void* works
                                                     RF_W8A16_WS_COUNTER_BYTES)
                          : nullptr;
   ka.amax_slots = nullptr;
+  // Contiguous strip ranges per XCD only where a group-wise scale's line
+  // over-fetch is a large share of the traffic: 32- and 64-wide groups (a
+  // scale row per 16 or 32 weight bytes of a channel) on launches of at least
+  // 16 MB of weights.  Graph-timed on MI355X, group size 32: Qwen3-8B gate,
+  // up and down at M = 1 11..12% faster, at M = 16 2..3%; launches of 8 MB or
+  // less 1..3% slower, and int8 q / o at M = 1..4 7..9% slower, so every other
+  // launch keeps the hardware's order.
+  int64_t wbytes = 0;
+  for (int i = 0; i < pr.nproj; ++i) wbytes += (int64_t)pr.proj[i].N * pr.K / 2;
+  const bool xcd = pr.wf == kWfInt4Grp && pr.gshift <= 1 && wbytes >= ((int64_t)16 << 20);
+  ka.xcd_run = xcd ? p.groups / 8 : 0;
   return ka;
 }
 
@@ -798,7 +828,7 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
   if (pr.nproj < 1 || pr.nproj > kMaxProj) return hipErrorInvalidValue;
   GemvKernelArgs ka = make_args(pr, p, workspace);
   if (pr.wf != kWfInt8) {
-    if (am) return hipErrorInvalidValue;
+    if (am || (pr.wf == kWfInt4Grp && pr.nproj != 1)) return hipErrorInvalidValue;
     return pr.wf == kWfInt4 ? launch_gemv4_cfg<kWfInt4>(ka, p, stream)
                             : launch_gemv4_cfg<kWfInt4Grp>(ka, p, stream);
   }

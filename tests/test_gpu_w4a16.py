@@ -275,3 +275,26 @@ def test_w4a16_random_shapes(case):
     rows = None if m <= 16 else np.r_[0:8, m - 8:m]
     check(y, x, q, s, label=f"w4 random {m}x{n}x{k} gs={gs}", rows=rows)
 
+
+
+# Group-wise launches of >= 16 MiB of weights with 32- or 64-wide groups run
+# with each XCD's workgroups on one contiguous strip range: a workgroup count
+# with a remainder mod 8 (1025, 129, 188), a ragged last group (257 strips,
+# two per workgroup), and K splits of 2 and 4.
+XCD_GROUPED = [
+    (1, 16400, 2048, 32), (16, 4112, 8192, 32), (12, 6000, 6144, 32),
+    (16, 4096, 12288, 32), (16, 2048, 16384, 64), (5, 16384, 2048, 64),
+]
+
+
+@pytest.mark.parametrize("m,n,k,gs", XCD_GROUPED)
+def test_w4a16_xcd_grouped_launches(m, n, k, gs):
+    _say(f"w4a16 xcd-grouped M={m} N={n} K={k} gs={gs}")
+    assert n * k // 2 >= 16 << 20
+    q, s = make_w4(n, k, gs, 5)
+    x = o8.make_activation(o8.derive_seed(5, "x4x", m, n, k), m, k)
+    packed = rf.pack_weight_int4(_dev(q))
+    y = run(x, q, s, packed=packed)
+    check(y, x, q, s, label=f"w4 xcd {m}x{n}x{k} gs={gs}")
+    y2 = run(x, q, s, packed=packed)
+    assert (y.view(np.uint16) == y2.view(np.uint16)).all()
