@@ -313,6 +313,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   // argument loads need not wait for the remapped group.
   int pi = 0;
   if (!GS) {
+    // The projection's fields are loaded once pi is known, a second
+    // scalar-memory trip.  Reading one field of each 64-byte argument line
+    // with the first loads (the loop below reads the group0 of projections
+    // 1..3) brings every line into the scalar cache, so that trip hits it.
+    __asm__ volatile("" ::"s"(a.M), "s"(a.proj[0].group0), "s"(a.kb_per_split));
 #pragma unroll
     for (int i = 1; i < kMaxProj; ++i)
       if (i < a.nproj && group >= a.proj[i].group0) pi = i;
