@@ -5,6 +5,7 @@ schemas and error paths); `-m gpu` runs the parity tests on an MI355X.
 """
 from __future__ import annotations
 
+import contextlib
 import sys
 from pathlib import Path
 
@@ -29,3 +30,24 @@ def pytest_collection_modifyitems(config, items):
         skip = pytest.mark.skip(reason="no HIP device visible")
         for it in gpu_items:
             it.add_marker(skip)
+
+
+@contextlib.contextmanager
+def fresh_hip_stream():
+    """A HIP stream made with hipStreamCreate (through the HIP runtime torch
+    loaded) and wrapped for torch: unlike torch.cuda.Stream(), which hands
+    out streams from a fixed pool, its handle is new to the W8A16 op's
+    per-stream workspace cache.  Synchronized and destroyed on exit."""
+    import ctypes
+    import os
+
+    import torch
+
+    hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+    handle = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(handle)) == 0
+    try:
+        yield torch.cuda.ExternalStream(handle.value)
+    finally:
+        assert hip.hipStreamSynchronize(handle) == 0
+        assert hip.hipStreamDestroy(handle) == 0

@@ -19,6 +19,7 @@ import rhinoforge_amd as rf
 from rhinoforge_amd import capi
 from oracle import w8a16 as o
 import planner_cases
+from conftest import fresh_hip_stream
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -967,3 +968,40 @@ def test_random_wide_launch_shapes(case):
         assert tuple(y.shape) == (m, ns[j])
         assert_parity(y.cpu().numpy(), x, q, s, b, rows=rows, label=f"proj {j} N={ns[j]}")
 
+
+
+def test_workspace_grows_on_a_fresh_stream():
+    """The torch ops call the C ABI with the stream's cached workspace first
+    (16 MB on a new stream) and grow it only when the call is refused with
+    EWORKSPACE.  (256, 4096, 8192) plans a 5-way split 128x128 GEMM whose
+    partials take 20 MB: on a fresh stream the first call of each op is
+    refused, grown and repeated.  Checked against the oracle on sampled rows
+    and, for every op, bit-identical to the same call on the default stream."""
+    m, n, k = 256, 4096, 8192
+    plan = capi.plan(m, [n], k, cus=256)
+    assert plan["workspace_bytes"] > (16 << 20), plan
+    _say(f"workspace growth M={m} N={n} K={k}: {plan['name']}, {plan['splits']} splits")
+    x, q, s, b = make_case(m, n, k, seed=23, bias=True)
+    xd, packed, sd, bd = _to_dev(x), rf.pack_weight(_to_dev(q)), _to_dev(s), _to_dev(b)
+    ref = rf.linear(xd, packed, sd, bd)
+    ref_multi = rf.linear_multi(xd, [packed, packed], [sd, sd], [bd, None])
+    torch.cuda.synchronize()
+    for op in ("linear", "linear_into", "linear_multi"):
+        with fresh_hip_stream() as stream:  # its workspace starts at the 16 MB default
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                if op == "linear":
+                    outs = [rf.linear(xd, packed, sd, bd)]
+                elif op == "linear_into":
+                    outs = [torch.empty_like(ref)]
+                    rf.linear_into(xd, packed, sd, bd, outs[0])
+                else:
+                    outs = rf.linear_multi(xd, [packed, packed], [sd, sd], [bd, None])
+            torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        want = ref_multi if op == "linear_multi" else [ref]
+        for got, exp in zip(outs, want):
+            assert torch.equal(got, exp), op
+    rows = np.r_[0:8, m - 8:m]
+    assert_parity(ref.cpu().numpy(), x, q, s, b, rows=rows, label="workspace growth")
+    assert_parity(ref_multi[1].cpu().numpy(), x, q, s, None, rows=rows, label="workspace growth multi")

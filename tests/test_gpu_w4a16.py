@@ -16,6 +16,7 @@ from rhinoforge_amd import capi
 from oracle import w4a16 as o4
 from oracle import w8a16 as o8
 import planner_cases
+from conftest import fresh_hip_stream
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -298,3 +299,28 @@ def test_w4a16_xcd_grouped_launches(m, n, k, gs):
     check(y, x, q, s, label=f"w4 xcd {m}x{n}x{k} gs={gs}")
     y2 = run(x, q, s, packed=packed)
     assert (y.view(np.uint16) == y2.view(np.uint16)).all()
+
+
+@pytest.mark.parametrize("gs", [0, 32])
+def test_w4a16_workspace_grows_on_a_fresh_stream(gs):
+    """A 5-way split int4 GEMM (256, 4096, 8192) needs 20 MB of workspace; on a
+    fresh stream (16 MB default) the first call is refused, the buffer grown
+    and the call repeated: bit-identical to the default stream's result, which
+    is checked against the oracle on sampled rows."""
+    m, n, k = 256, 4096, 8192
+    fmt = 2 if gs else 1
+    assert capi.plan(m, [n], k, fmt=fmt, cus=256)["workspace_bytes"] > (16 << 20)
+    _say(f"w4a16 workspace growth M={m} N={n} K={k} gs={gs}")
+    q, s = make_w4(n, k, gs, 6)
+    x = o8.make_activation(o8.derive_seed(6, "x4w", m, k), m, k)
+    packed, xd, sd = rf.pack_weight_int4(_dev(q)), _dev(x), _dev(s)
+    ref = rf.linear_w4a16(xd, packed, sd)
+    torch.cuda.synchronize()
+    with fresh_hip_stream() as stream:
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            y = rf.linear_w4a16(xd, packed, sd)
+        torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    check(ref.cpu().numpy(), x, q, s, label=f"w4 workspace growth gs={gs}", rows=np.r_[0:8, m - 8:m])
