@@ -346,7 +346,7 @@ int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_
     out->tile_m = p.bm;
     out->tile_n = p.bn;
     out->splits = p.splits;
-    out->waves = 4;
+    out->waves = rf::gemm_cfg_waves(p.cfg);
     out->workgroups = p.tiles_m * p.tiles_n * p.splits;
     out->workspace_bytes = rf::gemm_workspace_bytes(p);
     snprintf(out->name, sizeof(out->name), "gemm %s", rf::gemm_cfg_name(p.cfg, format, (int)M));

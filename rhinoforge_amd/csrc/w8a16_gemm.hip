@@ -212,9 +212,16 @@ __device__ __forceinline__ void store_tile(const TileTarget& t, const floatx4 (&
 // MFMAs (sched_group_barrier), and the wavefront runs its MFMA section at
 // raised issue priority (s_setprio 1).  Same arithmetic in the same order;
 // chosen where two wavefronts per SIMD are resident (see plan_gemm).
+//
+// KG: K groups per workgroup (1 or 2).  With two, the workgroup runs two
+// WAVES_M x WAVES_N grids of wavefronts; group g multiplies K blocks g,
+// g + 2, ... of the split (each stage holds one block per group), so a
+// launch of one tile per CU still keeps two wavefronts on every SIMD, each
+// with the instruction mix of the one-group tile.  At the end group 1 hands
+// its accumulators to group 0 through LDS, which adds them (fixed order).
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8,
-          bool IL = false, bool BR = false>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(OCC * WAVES_M * WAVES_N / 4, 8)))
+          bool IL = false, bool BR = false, int KG = 1>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64 * KG) __attribute__((amdgpu_waves_per_eu(OCC * WAVES_M * WAVES_N * KG / 4, 8)))
 void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -230,7 +237,10 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   // 1 x N grid no two wavefronts share a strip, so staging B in LDS only adds
   // a DMA write and a read per byte); LDS then holds A (and scales) only.
   constexpr int S_OFF = A_BYTES + (BR ? 0 : B_BYTES);
-  constexpr int STAGE = S_OFF + S_BYTES;
+  constexpr int SUB = S_OFF + S_BYTES;  // one K block's LDS
+  constexpr int STAGE = KG * SUB;       // one block per K group
+  static_assert(KG == 1 || (KG == 2 && !BR && !IL && WF == kWfInt8),
+                "two K groups: int8, B in LDS, plain schedule");
   constexpr int A_LOADS = A_BYTES / (NT * 16);
   constexpr int B_LOADS = BR ? 0 : B_BYTES / (NT * 16);
   constexpr int LOADS = A_LOADS + B_LOADS;
@@ -244,7 +254,10 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave: index within the wavefront's K group (kg_u, wave-uniform).
+  constexpr int NW = WAVES_M * WAVES_N;
+  const int wave = KG == 1 ? (tid >> 6) : (tid >> 6) % NW;
+  const int kg_u = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane((tid >> 6) / NW);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int tile = blockIdx.x;
   const int split = blockIdx.y;
@@ -303,9 +316,21 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   // Local K block i of this split = global K block kb0 + i, LDS stage i % STAGES.
   // may_tail = false (a constant at every call site) drops the K-tail check.
+  // Two K groups: stage i holds group g's block 2i + g at offset g * SUB; a
+  // block past the split's end is replaced by its last block (tail-safe
+  // addresses, never computed), so every stage issues the same loads.
   auto issue = [&](int i, bool may_tail) {
-    const int kb = kb0 + i;
-    const uint32_t st = lds0 + (i % STAGES) * STAGE;
+    int blk = i;
+    uint32_t st = lds0 + (i % STAGES) * STAGE;
+    if constexpr (KG == 2) {
+      blk = KG * i + kg_u;
+      st += kg_u * SUB;
+      if (blk >= nk) {
+        blk = nk - 1;
+        may_tail = true;
+      }
+    }
+    const int kb = kb0 + blk;
     if (may_tail && k_tail && kb == a.kblocks - 1) {
       // Last block with columns past K: those chunks load column 0 instead
       // and are zeroed after they land (fix_tail).
@@ -327,9 +352,10 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     if (GS && wave_u == 0)
       dma16s(soff, sbase + (int64_t)((2 * kb) >> a.gshift) * tt.N, st + S_OFF);
   };
-  auto fix_tail = [&](int i) {
+  auto fix_tail = [&](int i) {  // local K block i (two K groups: zeroed by its group)
     const int kb = kb0 + i;
     uint8_t* st = smem + (i % STAGES) * STAGE;
+    if constexpr (KG == 2) st = smem + ((i / KG) % STAGES) * STAGE + (i % KG) * SUB;
 #pragma unroll
     for (int l = 0; l < A_LOADS; ++l)
       if (kb * 64 + acol[l] >= a.K)
@@ -422,6 +448,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   };
   auto compute = [&](int i) {
     const uint8_t* st = smem + (i % STAGES) * STAGE;
+    if constexpr (KG == 2) st += kg_u * SUB;  // this wavefront's group's block
     if constexpr (WF != kWfInt8 && IL) {
       // The int8 interleaved schedule below with int4 B (and group-wise
       // scale reads among the first LDS reads).
@@ -555,9 +582,10 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
       compute_br(i, bq);
     }
   } else {
+  const int ns = (nk + KG - 1) / KG;  // stages: one block per K group each
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < nk) issue(s, true);
+    if (s < ns) issue(s, true);
   // Group-wise int4: wavefront 0 issues one more DMA per K block (scale rows).
   const bool extra = GS && wave_u == 0;
   // Steady state: the block issued (i + STAGES - 1 <= nk - 2) is never the
@@ -565,7 +593,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   // after block i; the loop carries no tail checks (their branches cost
   // about 4% on a 12288-deep K).
   int i = 0;
-  for (; i < nk - STAGES; ++i) {
+  for (; i < ns - STAGES; ++i) {
     if constexpr (STAGES - 2 >= 2) {
       if (extra) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (LOADS + 1)) : "memory");
       else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LOADS) : "memory");
@@ -577,12 +605,12 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     }
     barrier_lds();
     issue(i + STAGES - 1, false);
-    compute(i);
+    if (KG == 1 || KG * i + kg_u < nk) compute(i);
   }
   // The last STAGES blocks (or all of a short split): the block issued may be
   // the K tail, and fewer blocks remain in flight.
-  for (; i < nk; ++i) {
-    const int ahead = min(STAGES - 2, nk - 1 - i);  // blocks issued after i
+  for (; i < ns; ++i) {
+    const int ahead = min(STAGES - 2, ns - 1 - i);  // stages issued after i
     if (ahead >= 2) {
       if (extra) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (LOADS + 1)) : "memory");
       else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LOADS) : "memory");
@@ -592,12 +620,37 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     } else {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    if (k_tail && kb0 + i == a.kblocks - 1) fix_tail(i);
+    if constexpr (KG == 1) {
+      if (k_tail && kb0 + i == a.kblocks - 1) fix_tail(i);
+    } else {
+      if (k_tail && kb0 + nk - 1 == a.kblocks - 1 && i == (nk - 1) / KG && kg_u == (nk - 1) % KG)
+        fix_tail(nk - 1);
+    }
     barrier_lds();
     // Everyone is past compute(i-1): its stage can be refilled.
-    if (i + STAGES - 1 < nk) issue(i + STAGES - 1, true);
-    compute(i);
+    if (i + STAGES - 1 < ns) issue(i + STAGES - 1, true);
+    if (KG == 1 || KG * i + kg_u < nk) compute(i);  // none past the split's end
   }
+  }
+  if constexpr (KG == 2) {
+    // Every wavefront is past its last compute, so the stages are free: group
+    // 1 leaves its accumulators there and group 0 adds them to its own.
+    static_assert(NW * TM * TN * 64 * 16 <= STAGES * STAGE, "hand-off fits the stages");
+    barrier_lds();
+    floatx4* red = reinterpret_cast<floatx4*>(smem);
+    if (kg_u == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) red[((wave * TM + i) * TN + j) * 64 + lane] = acc[i][j];
+    }
+    barrier_lds();
+    if (kg_u == 0) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = acc[i][j] + red[((wave * TM + i) * TN + j) * 64 + lane];
+    }
   }
 
   if (a.splits > 1) {
@@ -609,19 +662,21 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     const __amdgpu_buffer_rsrc_t pr =
         partial_rsrc(a.partial, (uint32_t)((uint64_t)a.splits * tiles * TILE_F * 4));
     const uint32_t own = ((uint32_t)split * tiles + tile) * TILE_F * 4;
+    if (kg_u == 0) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t off = ((((wave * TM + i) * TN + j) * 4 + r) * 64 + lane) * 4;
-          // Copy the element out first: a bit cast of the vector-element
-          // lvalue itself reads element 0 whatever r is.
-          const float v = acc[i][j][r];
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pr, own + off, 0,
-                                                kCoherent);
-        }
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t off = ((((wave * TM + i) * TN + j) * 4 + r) * 64 + lane) * 4;
+            // Copy the element out first: a bit cast of the vector-element
+            // lvalue itself reads element 0 whatever r is.
+            const float v = acc[i][j][r];
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pr, own + off,
+                                                  0, kCoherent);
+          }
+    }
     __shared__ uint32_t is_last;
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores landed
     barrier_lds();
@@ -634,7 +689,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     if (!is_last) return;
     // Last to arrive: sum every split's partial (its own included, read
     // back) in split order, so the result does not depend on arrival order.
-    for (int sp = 0; sp < a.splits; ++sp) {
+    for (int sp = 0; sp < a.splits && kg_u == 0; ++sp) {
       const uint32_t base = ((uint32_t)sp * tiles + tile) * TILE_F * 4;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -652,6 +707,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
       __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
+  if (kg_u != 0) return;  // group 0 holds the tile's sums
   const bool full = m0 + BM <= a.M && (strip0 + B_TILES) * 16 <= tt.N;
   store_tile<TM, TN, !GS>(tt, acc, m0 + wm * WM, (strip0 + wn * TN) * 16, lane, a.M, full);
 }
@@ -788,14 +844,14 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void w8a16_gemm_dma_kernel(
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int WF = kWfInt8,
-          bool IL = false, bool BR = false>
+          bool IL = false, bool BR = false, int KG = 1>
 hipError_t launch_v3_t(const GemmKernelArgs& ka, hipStream_t stream) {
   const int64_t tiles = (int64_t)ka.tiles_m * ka.tiles_n;
   if (tiles <= 0 || tiles > 0x7fffffff || ka.splits < 1 || ka.splits > 65535 ||
       !v3_offsets_fit(ka, BM, BN))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, WF, IL, BR>),
-                     dim3((unsigned)tiles, (unsigned)ka.splits), dim3(WAVES_M * WAVES_N * 64), 0,
+  hipLaunchKernelGGL((w8a16_gemm_v3_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, WF, IL, BR, KG>),
+                     dim3((unsigned)tiles, (unsigned)ka.splits), dim3(WAVES_M * WAVES_N * 64 * KG), 0,
                      stream, ka);
   return hipGetLastError();
 }
@@ -825,6 +881,9 @@ enum GemmCfgId {
   kV3M128N128IL,  // kV3M128N128 with the interleaved MFMA schedule: 1..2 tiles per CU
   kV3M32N128,     // 4 wavefronts 1x4, 4 stages, 3 workgroups/CU: M <= 32, >= 0.75 tiles per CU
   kV3M32N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: M <= 32, >= 0.75 tiles per CU
+  kV3M128N128KG,  // two K groups of 4 wavefronts, 3 stages, 1 workgroup/CU: int8 M 128..512,
+  kV3M64N128KG,   //   launches of few tiles (see plan_gemm), 128x128 / 64x128 / 64x64 tiles
+  kV3M64N64KG,    //   (64x64: 4 stages)
   kGemmCfgCount
 };
 
@@ -832,7 +891,13 @@ enum GemmCfgId {
 constexpr int kGemmTile[kGemmCfgCount][3] = {{128, 256, 2}, {128, 128, 3}, {128, 128, 2},
                                              {64, 256, 2},  {128, 128, 1}, {32, 64, 4},
                                              {64, 64, 4},   {128, 128, 3}, {32, 128, 3},
-                                             {32, 256, 2}};
+                                             {32, 256, 2},  {128, 128, 1}, {64, 128, 1},
+                                             {64, 64, 1}};
+
+// Wavefronts per workgroup of a configuration.
+int gemm_cfg_waves(int cfg) {
+  return (cfg == kV3M128N128KG || cfg == kV3M64N128KG || cfg == kV3M64N64KG) ? 8 : 4;
+}
 
 // Short description of a configuration as it runs for weight format wf and
 // M rows (group-wise int4 at M >= 1024 runs the interleaved tile's register-B
@@ -850,6 +915,9 @@ const char* gemm_cfg_name(int cfg, int wf, int M) {
       return (wf == kWfInt4Grp && M >= 1024) ? "128x128 B-in-registers" : "128x128 interleaved";
     case kV3M32N128: return "32x128 4-stage";
     case kV3M32N256: return "32x256 3-stage";
+    case kV3M128N128KG: return "128x128 two K groups";
+    case kV3M64N128KG: return "64x128 two K groups";
+    case kV3M64N64KG: return "64x64 two K groups";
     default: return "?";
   }
 }
@@ -912,6 +980,50 @@ void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
 // launch to about three workgroups per CU -- the largest power of two <= 768
 // / tiles, at most 8, each split at least 8 K blocks -- or 64x256 tiles on
 // wide launches.
+// Launches of few tiles at M 128..512 (int8): the tile with two K groups,
+// which keeps two wavefronts on every SIMD at one workgroup per CU, in place
+// of a K split through memory.  Taken at <= 128 tiles of 128x128 unless K >=
+// 8192 with >= 96 of them (where the K-split plans with B in registers stay
+// ahead).  Among 128x128 / 64x128 / 64x64 and 1 / 2 / 4 splits that fit one
+// round (tiles x splits <= CUs, >= 16 K blocks per split) it takes the least
+// estimated time: the work per workgroup at 3.0 / 2.7 / 2.0 TFLOP/s per CU
+// (measured rates of the three tiles) plus 6 us for a split's hand-off.
+// Measured on 45 shapes (M 128..512, N 2048..8192, K 4096..12288, MI355X,
+// four rotated weight copies) against the plans below: -8.9% on average,
+// e.g. 2048 x 4096 at M 128 -35%, 4096 x 4096 at M 256 -16%, 4096 x 4096 at
+// M 512 -10.5%; none more than 2% slower.
+static bool plan_two_k_groups(int M, const int* Ns, int nproj, int K, int cus, int64_t t128,
+                              GemmPlan& out) {
+  const int kblocks = (int)ceil_div(K, 64);
+  if (t128 > 128 || (kblocks >= 128 && t128 >= 96)) return false;
+  struct Cand {
+    int cfg;
+    double rate;  // TFLOP/s per CU
+  };
+  const Cand cands[] = {{kV3M128N128KG, 3.0}, {kV3M64N128KG, 2.7}, {kV3M64N64KG, 2.0}};
+  double best = 0;
+  bool found = false;
+  for (const Cand& c : cands) {
+    GemmPlan p;
+    p.cfg = c.cfg;
+    set_tiles(p, M, Ns, nproj);
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    for (int s = 1; s <= 4; s *= 2) {
+      if (tiles * s > cus || kblocks < 16 * s || (s > 1 && tiles > kMaxSplitTiles)) continue;
+      const int kbs = (int)ceil_div(kblocks, s);
+      const double us = 2.0 * p.bm * p.bn * 64.0 * kbs / (c.rate * 1e6) + (s > 1 ? 6.0 : 0.0);
+      if (!found || us < best) {
+        found = true;
+        best = us;
+        p.kb_per_split = kbs;
+        p.splits = (int)ceil_div(kblocks, kbs);
+        out = p;
+      }
+    }
+  }
+  return found;
+}
+
 GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev, bool int4) {
   const int cus = dev.cus > 0 ? dev.cus : 256;
   if (M <= 32 && !int4) {
@@ -977,6 +1089,10 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   }
   const int64_t t128x256 = ceil_div(M, 128) * cols256;     // 128x256 tiles
   const int64_t t128 = ceil_div(M, 128) * cols128;         // 128x128 tiles
+  if (!int4 && M >= 128 && M <= 512) {
+    GemmPlan kgp;
+    if (plan_two_k_groups(M, Ns, nproj, K, cus, t128, kgp)) return kgp;
+  }
   GemmPlan p;
   if (M < 128) {
     p.cfg = kV3M64N256;
@@ -1154,6 +1270,9 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
     case kV3M128N128IL: return launch_v3_t<128, 128, 1, 4, 2, 3, kWfInt8, true>(ka, stream);
     case kV3M32N128: return launch_v3_t<32, 128, 1, 4, 4, 3>(ka, stream);
     case kV3M32N256: return launch_v3_t<32, 256, 1, 4, 3, 2>(ka, stream);
+    case kV3M128N128KG: return launch_v3_t<128, 128, 1, 4, 3, 1, kWfInt8, false, false, 2>(ka, stream);
+    case kV3M64N128KG: return launch_v3_t<64, 128, 1, 4, 3, 1, kWfInt8, false, false, 2>(ka, stream);
+    case kV3M64N64KG: return launch_v3_t<64, 64, 1, 4, 4, 1, kWfInt8, false, false, 2>(ka, stream);
     default: return hipErrorInvalidValue;
   }
 }

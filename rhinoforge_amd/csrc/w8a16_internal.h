@@ -89,6 +89,8 @@ size_t gemm_workspace_bytes(const GemmPlan& p);
 // weight format wf at M rows.
 void gemv_cfg_info(const GemvPlan& p, int M, bool int4, int* waves, bool* x_in_lds);
 const char* gemm_cfg_name(int cfg, int wf, int M);
+// Wavefronts per workgroup of a GEMM configuration.
+int gemm_cfg_waves(int cfg);
 
 // Fused argmax of a single-projection GEMV launch (M <= 64): the GEMV
 // stores every workgroup's best 64-bit key per row to `slots` (scratch,

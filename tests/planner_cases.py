@@ -166,16 +166,38 @@ GEMM_POLICY = [
     (200, 16400, 136, "gemm 128x128 interleaved", 128, 128, 1),
     # 128 <= M < 1024: 400 tiles of 128x256 tie with 800 of 128x128: 128x256
     (500, 25600, 136, "gemm 128x256 B-in-registers", 128, 256, 1),
-    # 128 <= M < 1024, N < 16384: 128x128 tiles, 3 stages
-    (300, 384, 1024, "gemm 128x128 3-stage", 128, 128, 1),
-    # 9 tiles, 64 K blocks: 4-way K split of 16 blocks
-    (300, 384, 4096, "gemm 128x128 3-stage", 128, 128, 4),
-    # 128 tiles, 17 K blocks: too short to split; K tail
-    (512, 4096, 1032, "gemm 128x128 3-stage", 128, 128, 1),
+    # 128 <= M < 1024, N < 16384: 128x128 tiles, 3 stages (M > 512: no K groups)
+    (600, 384, 1024, "gemm 128x128 3-stage", 128, 128, 1),
+    # 15 tiles, 64 K blocks: 4-way K split of 16 blocks
+    (600, 384, 4096, "gemm 128x128 3-stage", 128, 128, 4),
+    # 160 tiles, 17 K blocks: too short to split; K tail
+    (640, 4096, 1032, "gemm 128x128 3-stage", 128, 128, 1),
     # 275 tiles (1..2 per CU): interleaved schedule
     (640, 7000, 520, "gemm 128x128 interleaved", 128, 128, 1),
-    # 16 tiles, 33 K blocks: 2-way split, K tail in split 1
-    (200, 1000, 2056, "gemm 128x128 3-stage", 128, 128, 2),
+    # 40 tiles, 33 K blocks: 2-way split, K tail in split 1
+    (600, 1000, 2056, "gemm 128x128 3-stage", 128, 128, 2),
+    # M 128..512, <= 128 tiles of 128x128: two K groups, tile and split by the
+    # estimated time (one round, >= 16 K blocks per split)
+    (300, 384, 1024, "gemm 64x64 two K groups", 64, 64, 1),      # 30 tiles, 16 K blocks
+    (200, 1000, 2056, "gemm 64x64 two K groups", 64, 64, 1),     # ragged M/N, K tail
+    (128, 2048, 4096, "gemm 64x64 two K groups", 64, 64, 4),     # 64 tiles, 4-way split
+    (512, 4096, 4096, "gemm 64x128 two K groups", 64, 128, 1),   # 256 tiles, one per CU
+    (512, 4096, 1032, "gemm 64x128 two K groups", 64, 128, 1),   # 17 K blocks, K tail
+    (512, 1024, 5120, "gemm 64x128 two K groups", 64, 128, 4),   # Qwen3-VL-32B k at M = 512
+    (256, 4096, 12288, "gemm 128x128 two K groups", 128, 128, 4),
+    (384, 2048, 12288, "gemm 128x128 two K groups", 128, 128, 4),  # 48 tiles, 192 workgroups
+    # 18 K blocks with a K tail: the tail block falls to the second K group
+    (300, 384, 1096, "gemm 64x64 two K groups", 64, 64, 1),
+    # 65 K blocks in 4 splits of 17: each split's last stage has one block (the
+    # other group reloads it and skips it); K tail in the last split's group 2
+    (128, 2048, 4104, "gemm 64x64 two K groups", 64, 64, 4),
+    (129, 1040, 3016, "gemm 64x64 two K groups", 64, 64, 2),    # ragged M/N, K tail, 2 splits
+    (512, 2056, 2120, "gemm 64x128 two K groups", 64, 128, 1),  # ragged N, 34 K blocks, K tail
+    # ... but not at K >= 8192 with >= 96 tiles, beyond 128 tiles, or below 16 K blocks
+    (256, 6144, 8192, "gemm 128x128 B-in-registers", 128, 128, 5),
+    (136, 8192, 8200, "gemm 128x128 B-in-registers", 128, 128, 4),
+    (384, 5504, 4096, "gemm 128x128 B-in-registers", 128, 128, 2),  # 129 tiles
+    (130, 520, 264, "gemm 128x128 3-stage", 128, 128, 1),
     # M < 128: 6 tiles, 4-way K split
     (100, 520, 4096, "gemm 64x256 3-stage", 64, 256, 4),
     # M >= 1024: 128 tiles of 128x128, 5-way K split (>= 24 blocks each)

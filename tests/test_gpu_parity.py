@@ -650,13 +650,16 @@ def test_op_errors_on_device():
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 1024, 8192), (1, 4096, 1024), (300, 384, 1024),
-                                   (48, 5120, 8192), (32, 8192, 5120), (32, 25600, 320)])
+                                   (48, 5120, 8192), (32, 8192, 5120), (32, 25600, 320),
+                                   (128, 2048, 4104)])
 def test_graph_capture_replays_match_eager(m, n, k):
     """The op inside a HIP graph: every replay (with eager work between replays)
     equals the eager result bit for bit.  (16, 1024, 8192) takes the split-K
-    GEMV path, (48, 5120, 8192) the 8-way split mid-M GEMM and (32, 8192, 5120)
-    the 4-way split 32x64 tile, whose counters must be left zeroed for the next
-    replay; (32, 25600, 320) the unsplit 32x128 tile."""
+    GEMV path, (48, 5120, 8192) the 8-way split mid-M GEMM, (32, 8192, 5120)
+    the 4-way split 32x64 tile and (128, 2048, 4104) the 4-way split 64x64
+    tile with two K groups, whose counters must be left zeroed for the next
+    replay; (32, 25600, 320) the unsplit 32x128 tile, (300, 384, 1024) the
+    unsplit 64x64 tile with two K groups."""
     _say(f"graph capture M={m} N={n} K={k}")
     x, q, s, b = make_case(m, n, k, seed=17, bias=True)
     xd, packed, sd, bd = _to_dev(x), rf.pack_weight(_to_dev(q)), _to_dev(s), _to_dev(b)
@@ -970,14 +973,38 @@ def test_random_wide_launch_shapes(case):
 
 
 
+def test_linear_multi_two_k_groups():
+    """Three ragged projections at M = 256 (K = 4104, a K tail) in one launch of
+    the 64x64 tile with two K groups: every row of every output against the
+    oracle, and bit-identical to a second call."""
+    m, k = 256, 4104
+    ns = [1000, 520, 520]
+    plan = capi.plan(m, ns, k, cus=256)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert plan["name"] == "gemm 64x64 two K groups", plan
+    _say(f"linear_multi two K groups M={m} N={ns} K={k}")
+    cases = [make_case(m, n, k, seed=40 + i, bias=(i == 0)) for i, n in enumerate(ns)]
+    x = cases[0][0]
+    xd = _to_dev(x)
+    packed = [rf.pack_weight(_to_dev(c[1])) for c in cases]
+    scales = [_to_dev(c[2]) for c in cases]
+    biases = [None if c[3] is None else _to_dev(c[3]) for c in cases]
+    ys = rf.linear_multi(xd, packed, scales, biases)
+    again = rf.linear_multi(xd, packed, scales, biases)
+    torch.cuda.synchronize()
+    for i, (c, y, y2) in enumerate(zip(cases, ys, again)):
+        assert torch.equal(y, y2), i
+        assert_parity(y.cpu().numpy(), x, c[1], c[2], c[3], label=f"two K groups proj {i}")
+
+
 def test_workspace_grows_on_a_fresh_stream():
     """The torch ops call the C ABI with the stream's cached workspace first
     (16 MB on a new stream) and grow it only when the call is refused with
-    EWORKSPACE.  (256, 4096, 8192) plans a 5-way split 128x128 GEMM whose
-    partials take 20 MB: on a fresh stream the first call of each op is
+    EWORKSPACE.  (600, 4096, 8192) plans a 3-way split 128x128 GEMM whose
+    partials take 30 MB: on a fresh stream the first call of each op is
     refused, grown and repeated.  Checked against the oracle on sampled rows
     and, for every op, bit-identical to the same call on the default stream."""
-    m, n, k = 256, 4096, 8192
+    m, n, k = 600, 4096, 8192
     plan = capi.plan(m, [n], k, cus=256)
     assert plan["workspace_bytes"] > (16 << 20), plan
     _say(f"workspace growth M={m} N={n} K={k}: {plan['name']}, {plan['splits']} splits")
