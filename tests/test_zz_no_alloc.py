@@ -67,7 +67,7 @@ SEQUENCES = [
     # GEMV: M=16, K=12288 takes a 4-way K split; then M=4, one 1024-wide weight
     # (64 strips: 4-way split)
     ((16, [1024, 512, 256], 12288, capi.KERNEL_AUTO), (4, [1024], 4096, capi.KERNEL_AUTO)),
-    # GEMM: M=512 k/v-like (64 tiles of 128x128, K split) then M=300, one weight
+    # GEMM: M=512 k/v-like (64 tiles of 128x128: two K groups, K split) then M=300, one weight
     ((512, [1024, 1024], 5120, capi.KERNEL_AUTO), (300, [512], 2048, capi.KERNEL_GEMM)),
     # the mid-M GEMM tiles (M <= 64, K split to ~3 workgroups per CU), forced
     ((40, [2048, 1024], 4096, capi.KERNEL_GEMM), (24, [1024], 2048, capi.KERNEL_GEMM)),
