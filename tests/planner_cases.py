@@ -146,8 +146,8 @@ GEMV_INT4_POLICY = [
 
 # GEMM (forced).
 GEMM_POLICY = [
-    # M < 128: 64x256 tiles
-    (100, 520, 1032, "gemm 64x256 3-stage", 64, 256, 1),
+    # M < 128 beyond 128 tile columns of 128: 64x256 tiles
+    (100, 16520, 1032, "gemm 64x256 3-stage", 64, 256, 1),
     # M >= 1024, 520 tiles of 128x128 (3 per CU) cost less than 264 of 128x256
     (1024, 8200, 264, "gemm 128x128 B-in-registers", 128, 128, 1),
     # 768 tiles of 128x128 (3 per CU): one round of 384 128x256 tiles; K tail
@@ -198,8 +198,13 @@ GEMM_POLICY = [
     (136, 8192, 8200, "gemm 128x128 B-in-registers", 128, 128, 4),
     (384, 5504, 4096, "gemm 128x128 B-in-registers", 128, 128, 2),  # 129 tiles
     (130, 520, 264, "gemm 128x128 3-stage", 128, 128, 1),
-    # M < 128: 6 tiles, 4-way K split
-    (100, 520, 4096, "gemm 64x256 3-stage", 64, 256, 4),
+    # M < 128, 130 tile columns at K >= 8192: 64x256, 3-way K split
+    (100, 16520, 8192, "gemm 64x256 3-stage", 64, 256, 3),
+    # M 65..127 with few tiles: two K groups
+    (100, 520, 1032, "gemm 64x64 two K groups", 64, 64, 1),
+    (80, 1024, 4096, "gemm 64x64 two K groups", 64, 64, 4),
+    (112, 4096, 8192, "gemm 64x128 two K groups", 64, 128, 4),
+    (65, 2056, 4104, "gemm 64x128 two K groups", 64, 128, 4),  # one row in the second m-tile
     # M >= 1024: 128 tiles of 128x128, 5-way K split (>= 24 blocks each)
     (1024, 2048, 8192, "gemm 128x128 B-in-registers", 128, 128, 5),
     # 160 tiles, 3-way split (two per CU): 128x128 with B in registers; K tail
