@@ -881,7 +881,7 @@ enum GemmCfgId {
   kV3M128N128IL,  // kV3M128N128 with the interleaved MFMA schedule: 1..2 tiles per CU
   kV3M32N128,     // 4 wavefronts 1x4, 4 stages, 3 workgroups/CU: M <= 32, >= 0.75 tiles per CU
   kV3M32N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: M <= 32, >= 0.75 tiles per CU
-  kV3M128N128KG,  // two K groups of 4 wavefronts, 3 stages, 1 workgroup/CU: int8 M 65..512,
+  kV3M128N128KG,  // two K groups of 4 wavefronts, 3 stages, 1 workgroup/CU: int8 M 65..2048,
   kV3M64N128KG,   //   launches of few tiles (see plan_gemm), 128x128 / 64x128 / 64x64 tiles
   kV3M64N64KG,    //   (64x64: 4 stages)
   kGemmCfgCount
@@ -980,7 +980,7 @@ void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
 // launch to about three workgroups per CU -- the largest power of two <= 768
 // / tiles, at most 8, each split at least 8 K blocks -- or 64x256 tiles on
 // wide launches.
-// Launches of few tiles at M 65..512 (int8): the tile with two K groups,
+// Launches of few tiles at M 65..2048 (int8): the tile with two K groups,
 // which keeps two wavefronts on every SIMD at one workgroup per CU, in place
 // of a K split through memory.  Taken at <= 128 tiles of 128x128 unless K >=
 // 8192 with >= 96 of them (where the K-split plans with B in registers stay
@@ -992,12 +992,18 @@ void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
 // four rotated weight copies) against the plans below: -8.9% on average,
 // e.g. 2048 x 4096 at M 128 -35%, 4096 x 4096 at M 256 -16%, 4096 x 4096 at
 // M 512 -10.5%; none more than 2% slower.  At M 80..112 (N 1024..4096, K
-// 4096..8192) against the 64x256 tiles: -22..-41%.  Beyond M 512 the forms
-// lost up to 6% at K 8192, so they stop there.
+// 4096..8192) against the 64x256 tiles: -22..-41%.  At M 640..2048 (N 512..
+// 2048, K 2048..5120) with >= 0.75 workgroups per CU: -3.5..-33% (e.g. 1024 x
+// 4096 at M 2048 27.8 -> 24.9 us); there K 8192, more splits or fewer
+// workgroups lost up to 16%, hence the extra conditions.
 static bool plan_two_k_groups(int M, const int* Ns, int nproj, int K, int cus, int64_t t128,
                               GemmPlan& out) {
   const int kblocks = (int)ceil_div(K, 64);
   if (t128 > 128 || (kblocks >= 128 && t128 >= 96)) return false;
+  // Beyond M 512 only where the forms measured faster: K <= 5120, at most
+  // two K splits and >= 0.75 workgroups per CU.
+  const bool beyond = M > 512;
+  if (beyond && kblocks > 80) return false;
   struct Cand {
     int cfg;
     double rate;  // TFLOP/s per CU
@@ -1012,6 +1018,7 @@ static bool plan_two_k_groups(int M, const int* Ns, int nproj, int K, int cus, i
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     for (int s = 1; s <= 4; s *= 2) {
       if (tiles * s > cus || kblocks < 16 * s || (s > 1 && tiles > kMaxSplitTiles)) continue;
+      if (beyond && (s > 2 || 4 * tiles * s < 3LL * cus)) continue;
       const int kbs = (int)ceil_div(kblocks, s);
       const double us = 2.0 * p.bm * p.bn * 64.0 * kbs / (c.rate * 1e6) + (s > 1 ? 6.0 : 0.0);
       if (!found || us < best) {
@@ -1091,7 +1098,7 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   }
   const int64_t t128x256 = ceil_div(M, 128) * cols256;     // 128x256 tiles
   const int64_t t128 = ceil_div(M, 128) * cols128;         // 128x128 tiles
-  if (!int4 && M <= 512) {  // M >= 65 here
+  if (!int4 && M <= 2048) {  // M >= 65 here
     GemmPlan kgp;
     if (plan_two_k_groups(M, Ns, nproj, K, cus, t128, kgp)) return kgp;
   }

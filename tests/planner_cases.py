@@ -205,6 +205,13 @@ GEMM_POLICY = [
     (80, 1024, 4096, "gemm 64x64 two K groups", 64, 64, 4),
     (112, 4096, 8192, "gemm 64x128 two K groups", 64, 128, 4),
     (65, 2056, 4104, "gemm 64x128 two K groups", 64, 128, 4),  # one row in the second m-tile
+    # M 513..2048, K <= 5120, few tiles and >= 0.75 workgroups per CU: two K groups
+    (1024, 1024, 4096, "gemm 64x64 two K groups", 64, 64, 1),
+    (1500, 1000, 4104, "gemm 64x128 two K groups", 64, 128, 1),  # ragged M, N and K
+    (1024, 512, 4096, "gemm 64x64 two K groups", 64, 64, 2),
+    (2048, 1024, 5120, "gemm 64x128 two K groups", 64, 128, 1),
+    (640, 1024, 4096, "gemm 128x128 3-stage", 128, 128, 4),  # 160 workgroups: fewer than 0.75 per CU
+    (2048, 1024, 5128, "gemm 128x128 B-in-registers", 128, 128, 3),  # K > 5120
     # M >= 1024: 128 tiles of 128x128, 5-way K split (>= 24 blocks each)
     (1024, 2048, 8192, "gemm 128x128 B-in-registers", 128, 128, 5),
     # 160 tiles, 3-way split (two per CU): 128x128 with B in registers; K tail
