@@ -881,7 +881,7 @@ enum GemmCfgId {
   kV3M128N128IL,  // kV3M128N128 with the interleaved MFMA schedule: 1..2 tiles per CU
   kV3M32N128,     // 4 wavefronts 1x4, 4 stages, 3 workgroups/CU: M <= 32, >= 0.75 tiles per CU
   kV3M32N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: M <= 32, >= 0.75 tiles per CU
-  kV3M128N128KG,  // two K groups of 4 wavefronts, 3 stages, 1 workgroup/CU: int8 M 65..2048,
+  kV3M128N128KG,  // two K groups of 4 wavefronts, 3 stages, 1 workgroup/CU: int8 M 33..2048,
   kV3M64N128KG,   //   launches of few tiles (see plan_gemm), 128x128 / 64x128 / 64x64 tiles
   kV3M64N64KG,    //   (64x64: 4 stages)
   kGemmCfgCount
@@ -979,8 +979,8 @@ void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
 // M 33..64 (int8): 64x64 tiles (four per CU) and a K split that brings the
 // launch to about three workgroups per CU -- the largest power of two <= 768
 // / tiles, at most 8, each split at least 8 K blocks -- or 64x256 tiles on
-// wide launches.
-// Launches of few tiles at M 65..2048 (int8): the tile with two K groups,
+// wide launches, or the 64x64 tile with two K groups (below).
+// Launches of few tiles at M 33..2048 (int8): the tile with two K groups,
 // which keeps two wavefronts on every SIMD at one workgroup per CU, in place
 // of a K split through memory.  Taken at <= 128 tiles of 128x128 unless K >=
 // 8192 with >= 96 of them (where the K-split plans with B in registers stay
@@ -1004,6 +1004,11 @@ static bool plan_two_k_groups(int M, const int* Ns, int nproj, int K, int cus, i
   // two K splits and >= 0.75 workgroups per CU.
   const bool beyond = M > 512;
   if (beyond && kblocks > 80) return false;
+  // At M 33..64 only the 64x64 form with four K splits over <= 64 tiles
+  // (K >= 4096): -8..-14% against the 64x64 4-stage tile with 8 splits at
+  // N 1024..4096, K 4096..8192; at N 5120 / 8192 mixed (-7..+4%).
+  const bool one_row = M <= 64;
+  if (one_row && kblocks < 64) return false;
   struct Cand {
     int cfg;
     double rate;  // TFLOP/s per CU
@@ -1016,6 +1021,7 @@ static bool plan_two_k_groups(int M, const int* Ns, int nproj, int K, int cus, i
     p.cfg = c.cfg;
     set_tiles(p, M, Ns, nproj);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    if (one_row && (c.cfg != kV3M64N64KG || 4 * tiles > cus)) continue;
     for (int s = 1; s <= 4; s *= 2) {
       if (tiles * s > cus || kblocks < 16 * s || (s > 1 && tiles > kMaxSplitTiles)) continue;
       if (beyond && (s > 2 || 4 * tiles * s < 3LL * cus)) continue;
@@ -1080,6 +1086,8 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
       p.splits = (int)ceil_div(kblocks, p.kb_per_split);
       return p;
     }
+    GemmPlan kgp;
+    if (plan_two_k_groups(M, Ns, nproj, K, cus, /*t128=*/0, kgp)) return kgp;
     p.cfg = kV3M64N64;
     set_tiles(p, M, Ns, nproj);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;

@@ -200,6 +200,12 @@ GEMM_POLICY = [
     (130, 520, 264, "gemm 128x128 3-stage", 128, 128, 1),
     # M < 128, 130 tile columns at K >= 8192: 64x256, 3-way K split
     (100, 16520, 8192, "gemm 64x256 3-stage", 64, 256, 3),
+    # M 33..64, <= 64 tiles of 64x64, K >= 4096: 64x64 two K groups, 4 splits
+    (48, 1024, 4096, "gemm 64x64 two K groups", 64, 64, 4),
+    (33, 1000, 4104, "gemm 64x64 two K groups", 64, 64, 4),  # ragged N and K
+    (64, 4096, 8192, "gemm 64x64 two K groups", 64, 64, 4),
+    (48, 5120, 4096, "gemm 64x64 4-stage", 64, 64, 8),  # 80 tiles: more than 64
+    (64, 2048, 2048, "gemm 64x64 4-stage", 64, 64, 4),  # K < 4096
     # M 65..127 with few tiles: two K groups
     (100, 520, 1032, "gemm 64x64 two K groups", 64, 64, 1),
     (80, 1024, 4096, "gemm 64x64 two K groups", 64, 64, 4),
