@@ -522,6 +522,34 @@ def bench_cfg4(torch, rf):
     return rows
 
 
+# Launches of few tiles across M (the GEMM's two-K-group rules): Qwen3-8B
+# and Qwen3-VL-32B projections that leave most CUs without a whole tile.
+FEW_TILES = [(48, "8b q", 4096, 4096), (48, "8b k", 1024, 4096), (64, "8b q", 4096, 4096),
+             (96, "8b q", 4096, 4096), (96, "8b k", 1024, 4096), (96, "vl k", 1024, 5120),
+             (1024, "8b k", 1024, 4096), (1024, "vl k", 1024, 5120),
+             (2048, "8b k", 1024, 4096), (2048, "vl k", 1024, 5120)]
+
+
+def bench_few_tiles(torch, rf):
+    """Per-launch times of FEW_TILES through linear_into (AUTO), rotating
+    weight copies of >= 320 MB per shape (past the 256 MB Infinity Cache);
+    M >= 512 judged against MFMA, smaller M against HBM."""
+    rows = []
+    for m, name, n, k in FEW_TILES:
+        ncopies = max(4, -(-(320 << 20) // (n * k)))
+        cs = [make_layer(torch, rf, [(name, n, k)], seed=970 + c)[0] for c in range(ncopies)]
+        x = torch.randn(m, k, device="cuda").half()
+        y = torch.empty(m, n, device="cuda", dtype=torch.float16)
+        us = per_launch_us(torch, lambda c: rf.linear_into(x, c[3], c[4], None, y), cs,
+                           2 * ncopies)
+        rows.append(roofline_row({"M": m, "proj": name, "N": n, "K": k, "us": round(us, 2),
+                                  "plan": plan_name(m, n, k)},
+                                 "mfma" if m >= 512 else "hbm", nbytes(m, n, k), 2 * m * n * k))
+        del cs
+    torch.cuda.empty_cache()
+    return rows
+
+
 def bench_other_configs(torch, rf):
     """Per-launch timings of BASELINE configs 0, 2 and 4 and the W4A16 rows (not
     part of `value`); returns them and config 2's argmax case for cpu_baseline."""
@@ -732,7 +760,8 @@ def main():
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run three device-to-device copies of this many MB (the "
                          "known-size reference kernel for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--only", choices=("decode", "prefill", "cfg0", "cfg2", "cfg4", "w4a16"),
+    ap.add_argument("--only", choices=("decode", "prefill", "cfg0", "cfg2", "cfg4", "w4a16",
+                                       "few_tiles"),
                     help="run one section alone and print its result (a profiling aid: "
                          "its JSON line is not the benchmark line)")
     args = ap.parse_args()
@@ -768,6 +797,7 @@ def main():
             "cfg2": lambda: bench_cfg2(torch, rf)[0],
             "cfg4": lambda: bench_cfg4(torch, rf),
             "w4a16": lambda: bench_w4a16(torch, rf),
+            "few_tiles": lambda: bench_few_tiles(torch, rf),
         }
         print(json.dumps({"only": args.only, "result": sections[args.only]()}), flush=True)
         return
