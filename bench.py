@@ -522,9 +522,11 @@ def bench_cfg4(torch, rf):
     return rows
 
 
-# Launches of few tiles across M (the GEMM's two-K-group rules): Qwen3-8B
-# and Qwen3-VL-32B projections that leave most CUs without a whole tile.
-FEW_TILES = [(48, "8b q", 4096, 4096), (48, "8b k", 1024, 4096), (64, "8b q", 4096, 4096),
+# Launches of few tiles across M (the GEMV's 16-wavefront rule at M 17..32,
+# the GEMM's two-K-group rules above): Qwen3-8B and Qwen3-VL-32B projections
+# that leave most CUs without a whole tile.
+FEW_TILES = [(24, "8b k", 1024, 4096), (32, "8b k", 1024, 4096), (32, "vl k", 1024, 5120),
+             (48, "8b q", 4096, 4096), (48, "8b k", 1024, 4096), (64, "8b q", 4096, 4096),
              (96, "8b q", 4096, 4096), (96, "8b k", 1024, 4096), (96, "vl k", 1024, 5120),
              (1024, "8b k", 1024, 4096), (1024, "vl k", 1024, 5120),
              (2048, "8b k", 1024, 4096), (2048, "vl k", 1024, 5120)]

@@ -721,6 +721,7 @@ enum GemvCfgId {
   kG1x5W8U1,     // MT=1 NS=5 W=8  U=1
   kG1x6W8U1,     // MT=1 NS=6 W=8  U=1
   kG1x7W8U1,     // MT=1 NS=7 W=8  U=1
+  kG2x2W16U1,    // MT=2 NS=2 W=16 U=1  (int8, M 17..32 on <= 128 strips, 4-way K split)
   kGemvCfgCount
 };
 
@@ -734,6 +735,7 @@ constexpr GemvCfgDesc kGemvCfgs[kGemvCfgCount] = {
     {1, 2, 16, false}, {1, 4, 8, false}, {1, 4, 4, false}, {1, 2, 8, false},
     {2, 4, 4, false},  {2, 2, 8, false}, {2, 1, 8, false}, {4, 2, 8, false}, {4, 2, 4, false},
     {1, 3, 8, false},  {1, 5, 8, false}, {1, 6, 8, false}, {1, 7, 8, false},
+    {2, 2, 16, false},
 };
 
 bool lds_fits(int cfg, int M, int kb_per_split) {
@@ -761,6 +763,7 @@ hipError_t launch_gemv_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStrea
     case kG1x5W8U1: return launch_t<1, 5, 8, 1, false, true>(ka, p, stream);
     case kG1x6W8U1: return launch_t<1, 6, 8, 1, false, true>(ka, p, stream);
     case kG1x7W8U1: return launch_t<1, 7, 8, 1, false, true>(ka, p, stream);
+    case kG2x2W16U1: return launch_t<2, 2, 16, 1, false, true>(ka, p, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -967,7 +970,8 @@ GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev
 //   * K splits only where the strips alone cannot fill 256 CUs.
 // one_round: the int8 rules at M 5..16 that give a workgroup three to seven
 // strips (kG1x3W8U2 .. kG1x7W8U1, sized to about one or two workgroups per
-// CU); the int4 planner starts from the rules without them.
+// CU) and the 16-wavefront rule at M 17..32 (kG2x2W16U1); the int4 planner
+// starts from the rules without them.
 GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
                          bool one_round) {
   // Rules see the launch's strips of all projections together.
@@ -1055,6 +1059,14 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
       cfg = kG2x4W4U2;
     } else if (kblocks >= 128) {
       cfg = kG2x4W4U2;
+      splits = 4;
+    } else if (one_round && !strips_ge(129) && kblocks >= 64) {
+      // <= 128 strips, K 4096..8191 (int8): two strips per 16-wavefront
+      // workgroup and a 4-way K split (MI355X, 600 MB of rotated weights:
+      // Qwen3-8B k and v together, 2048 x 4096, at M 24 / 32 7.6 / 8.0
+      // instead of 9.7 / 11.1 us; k alone, 1024 x 4096, 6.9 / 7.4 instead
+      // of 7.7 / 8.3 us; 1024 x 5120 -4%).
+      cfg = kG2x2W16U1;
       splits = 4;
     } else if (!strips_ge(65)) {
       cfg = kG2x1W8U4;

@@ -77,6 +77,10 @@ GEMV_POLICY = [
     (20, 16384, 128, "gemv 2x4 strips, 4 waves", 32, 64, 1),
     # M 17..32, long K: 4-way K split
     (32, 640, 8192, "gemv 2x4 strips, 4 waves", 32, 64, 4),
+    # M 17..32, <=128 strips, K 4096..8191 (int8): two strips per 16-wave workgroup, 4-way split
+    (24, 1024, 4096, "gemv 2x2 strips, 16 waves", 32, 32, 4),
+    (32, 2040, 5128, "gemv 2x2 strips, 16 waves", 32, 32, 4),  # ragged N and K
+    (17, 2064, 4096, "gemv 2x2 strips, 8 waves", 32, 32, 1),  # 129 strips: the default
     # M 17..32, <=64 strips: 4-way K split
     (17, 1024, 512, "gemv 2x1 strips, 8 waves", 32, 16, 4),
     # M 17..32, default
