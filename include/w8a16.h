@@ -30,7 +30,10 @@
 extern "C" {
 #endif
 
-#define RF_W8A16_ABI_VERSION 3
+/* 4: rf_w8a16_plan applies the compute entry points' refusals (EALIGN,
+ * EKERNEL) and their GEMV -> GEMM fallback; the torch boundary's packed
+ * weight tensors are 3-D tiles [ceil(N/16), ceil(K/64 or 128), 1024]. */
+#define RF_W8A16_ABI_VERSION 4
 
 /* Status codes.  The torch op maps each to a RuntimeError with the message
  * from rf_w8a16_status_str (the reference raises TORCH_CHECK before any
@@ -71,7 +74,9 @@ typedef enum rf_w8a16_status {
 #define RF_W8A16_KERNEL_GEMV 1 /* decode GEMV / skinny GEMM, M <= 64 (AUTO: M <= 16, M <= 28
                                   with N*K <= 2^24, M <= 32 with N*K <= 2^23;
                                   W4A16: M <= 64)                             */
-#define RF_W8A16_KERNEL_GEMM 2 /* LDS-staged dequant-into-MFMA GEMM         */
+#define RF_W8A16_KERNEL_GEMM 2 /* prefill GEMM: x tiles staged in LDS by DMA, int8 weight
+                                  tiles dequantized into fp16 MFMA operands (from
+                                  registers on the large tiles, from LDS on the others) */
 
 /* Human-readable text for a status code; never NULL. */
 const char* rf_w8a16_status_str(int status);
@@ -127,8 +132,12 @@ typedef struct rf_w8a16_plan_info {
 /* Plan of a call with `count` projections of widths Ns sharing (M, K) and a
  * contiguous x (ldx = K), for `kernel` (AUTO / GEMV / GEMM) and weight
  * `format`, on a part with `cus` compute units (0: the current device's).
- * Returns RF_W8A16_OK, RF_W8A16_EINVAL or RF_W8A16_EKERNEL (as the compute
- * entry points would for that shape). */
+ * The plan is the one the compute entry points run for that call, with the
+ * same refusals: RF_W8A16_EINVAL (bad sizes; int4 with N % 16 or K % 64
+ * nonzero), RF_W8A16_EALIGN (int8 with K % 8 nonzero), RF_W8A16_EKERNEL
+ * (a forced GEMV at M > 64 or at a row stride ldx = K its 32-bit offsets
+ * cannot address -- AUTO then plans the GEMM, as the compute entry points
+ * run it -- or an int4 GEMM whose tile offsets overflow), else RF_W8A16_OK. */
 int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_t kernel,
                   int32_t format, int32_t cus, rf_w8a16_plan_info* out);
 
@@ -206,8 +215,11 @@ int rf_w8a16_linear_multi(const void* x, int64_t ldx, int32_t layout, const rf_w
  *   - Every call on one GPU shares that GPU's array.  Calls that overlap in
  *     time on one GPU (two streams, two host threads, two graphs replayed
  *     concurrently) race and must be ordered by the caller.
- *   - The counters start at zero (the first call on a device also clears
- *     them with a fill kernel on its stream) and every call leaves them zero. */
+ *   - The counters start at zero (the array is zero-initialized when the
+ *     library's code object loads; a first call on a device outside graph
+ *     capture also clears them with a fill kernel on its stream) and every
+ *     call leaves them zero.  A first call under graph capture records no
+ *     fill, so replays never reset counters other calls rely on. */
 #define RF_W8A16_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int rf_w8a16_linear_multi_noalloc(const void* x, int64_t ldx, int32_t layout,
                                   const rf_w8a16_proj* projs, int32_t count, int64_t M, int64_t K,

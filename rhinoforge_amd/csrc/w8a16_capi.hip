@@ -179,11 +179,12 @@ __global__ void zero_u4_kernel(uint4* p, int n) {
 }
 
 // Device address of the current device's scratch array, looked up once per
-// device (with that device current).  The first lookup also clears the
-// counter region with a fill kernel on `stream` (a fill kernel, not a
-// memset node, so that it replays correctly if the first call is captured
-// into a graph); every later call finds the counters zero, because each
-// call leaves them so.
+// device (with that device current).  A __device__ array without an
+// initializer is zero when the code object loads, so the counters start at
+// zero, and every call leaves them so.  The first lookup on an uncaptured
+// stream clears the counter region once more with a fill kernel (no memset
+// node); under graph capture it does not, since the fill would be recorded
+// into the graph and re-zero the shared counters on every replay.
 int noalloc_scratch(hipStream_t stream, void** out) {
   constexpr int kMaxDevices = 64;
   static std::atomic<void*> ptrs[kMaxDevices];
@@ -198,10 +199,14 @@ int noalloc_scratch(hipStream_t stream, void** out) {
     if (!p) {
       if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RF_W8A16_EHIP;
       if (!aligned(p, 256)) return RF_W8A16_EHIP;
-      constexpr int n = (int)(RF_W8A16_WS_COUNTER_BYTES / 16);
-      hipLaunchKernelGGL(zero_u4_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
-                         static_cast<uint4*>(p), n);
-      if (hipGetLastError() != hipSuccess) return RF_W8A16_EHIP;
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return RF_W8A16_EHIP;
+      if (cap == hipStreamCaptureStatusNone) {
+        constexpr int n = (int)(RF_W8A16_WS_COUNTER_BYTES / 16);
+        hipLaunchKernelGGL(zero_u4_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                           static_cast<uint4*>(p), n);
+        if (hipGetLastError() != hipSuccess) return RF_W8A16_EHIP;
+      }
       ptrs[dev].store(p, std::memory_order_release);
     }
   }
@@ -310,9 +315,14 @@ int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_
   int64_t ntotal = 0;
   for (int i = 0; i < count; ++i) {
     if (check_nk(Ns[i], K) != RF_W8A16_OK) return RF_W8A16_EINVAL;
+    if (int4 && Ns[i] % 16 != 0) return RF_W8A16_EINVAL;  // as rf_w4a16_linear
     n32[i] = (int)Ns[i];
     ntotal += Ns[i];
   }
+  // The compute entry points' other refusals for this shape (x contiguous:
+  // ldx = K).
+  if (int4 && K % 64 != 0) return RF_W8A16_EINVAL;
+  if (!int4 && K % 8 != 0) return RF_W8A16_EALIGN;
   rf::DeviceInfo dev;
   if (cus > 0) {
     dev.cus = cus;
@@ -321,9 +331,14 @@ int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_
     const int st = rf::device_info(&dev);
     if (st != RF_W8A16_OK) return st;
   }
-  if (kernel == RF_W8A16_KERNEL_AUTO) kernel = int4 ? auto_kernel_int4(M) : auto_kernel(M, ntotal, K);
+  if (kernel == RF_W8A16_KERNEL_AUTO) {
+    kernel = int4 ? auto_kernel_int4(M) : auto_kernel(M, ntotal, K);
+    if (kernel == RF_W8A16_KERNEL_GEMV && !rf::gemv_offsets_fit(M, K))
+      kernel = RF_W8A16_KERNEL_GEMM;  // the fallback the compute entry points take
+  }
   if (kernel != RF_W8A16_KERNEL_GEMV && kernel != RF_W8A16_KERNEL_GEMM) return RF_W8A16_EINVAL;
-  if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) return RF_W8A16_EKERNEL;
+  if (kernel == RF_W8A16_KERNEL_GEMV && (M > 64 || !rf::gemv_offsets_fit(M, K)))
+    return RF_W8A16_EKERNEL;
   memset(out, 0, sizeof(*out));
   out->kernel = kernel;
   if (kernel == RF_W8A16_KERNEL_GEMV) {
@@ -342,7 +357,13 @@ int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_
     snprintf(out->name, sizeof(out->name), "gemv %dx%d strips, %d waves%s", p.mt, p.ns, waves,
              xl ? ", x in LDS" : "");
   } else {
-    const rf::GemmPlan p = rf::plan_gemm((int)M, n32, count, (int)K, dev, int4);
+    const rf::GemmPlan p = rf::gemm_plan_for_stride(rf::plan_gemm((int)M, n32, count, (int)K, dev, int4),
+                                                    (int)M, n32, count, K, (int)K, int4);
+    // The int4 GEMM has no 64-bit-address kernel (rf_w4a16_linear refuses).
+    if (int4 && !rf::gemm_offsets_fit(p, K, (int)K, true)) {
+      memset(out, 0, sizeof(*out));
+      return RF_W8A16_EKERNEL;
+    }
     out->tile_m = p.bm;
     out->tile_n = p.bn;
     out->splits = p.splits;

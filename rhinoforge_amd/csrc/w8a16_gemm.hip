@@ -1198,11 +1198,27 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
 }
 
 bool gemm_offsets_fit(const GemmPlan& p, int64_t ldx, int K, bool int4) {
+  if (p.cfg == kDmaM128N128) return true;  // full per-lane addresses
   GemmKernelArgs ka;
   ka.ldx = ldx;
   ka.kblocks = (int)ceil_div(K, 64);
   ka.wtiles = int4 ? (int)ceil_div(K, kTileK4) : ka.kblocks;
   return v3_offsets_fit(ka, p.bm, p.bn);
+}
+
+// The v3 kernels address a tile with 32-bit offsets from its first row /
+// strip (row stride ldx); an int8 plan whose offsets could overflow runs the
+// 64-bit-address kernel, unsplit.  int4 plans are returned as they are (the
+// caller refuses them: there is no int4 64-bit-address kernel).
+GemmPlan gemm_plan_for_stride(const GemmPlan& plan, int M, const int* Ns, int nproj, int64_t ldx,
+                              int K, bool int4) {
+  GemmPlan p = plan;
+  if (int4 || gemm_offsets_fit(p, ldx, K, false)) return p;
+  p.cfg = kDmaM128N128;
+  set_tiles(p, M, Ns, nproj);
+  p.splits = 1;
+  p.kb_per_split = (int)ceil_div(K, 64);
+  return p;
 }
 
 size_t gemm_workspace_bytes(const GemmPlan& p) {
@@ -1259,18 +1275,13 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
       ka.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + RF_W8A16_WS_COUNTER_BYTES);
     }
   };
-  fill(p);
-  // The v3 kernels address a tile with 32-bit offsets from its first row /
-  // strip (row stride ldx); fall back to 64-bit addressing when those could
-  // overflow.
-  if (p.cfg != kDmaM128N128 && !v3_offsets_fit(ka, p.bm, p.bn)) {
-    if (pr.wf != kWfInt8) return hipErrorInvalidValue;  // int4 tiles are half the span: not reached
-    p.cfg = kDmaM128N128;
-    set_tiles(p, pr.M, ns, pr.nproj);
-    p.splits = 1;
-    p.kb_per_split = ka.kblocks;
-    fill(p);
+  // 64-bit addressing where the v3 kernels' 32-bit tile offsets could
+  // overflow (int8; int4 has no such kernel and its callers refuse first).
+  if (!gemm_offsets_fit(p, pr.ldx, pr.K, pr.wf != kWfInt8)) {
+    if (pr.wf != kWfInt8) return hipErrorInvalidValue;
+    p = gemm_plan_for_stride(p, pr.M, ns, pr.nproj, pr.ldx, pr.K, false);
   }
+  fill(p);
   if (p.splits > 1 && (!workspace || (int64_t)p.tiles_m * p.tiles_n > kMaxSplitTiles ||
                        gemm_workspace_bytes(p) >= (1ull << 31)))
     return hipErrorInvalidValue;

@@ -75,6 +75,10 @@ inline bool gemv_offsets_fit(int64_t M, int64_t ldx) {
 // and row stride (otherwise int8 launches take the 64-bit-address kernel;
 // int4 launches have none).
 bool gemm_offsets_fit(const GemmPlan& p, int64_t ldx, int K, bool int4);
+// The plan launch_gemm runs at row stride ldx: int8 plans whose offsets do
+// not fit become the 64-bit-address kernel (unsplit); int4 plans unchanged.
+GemmPlan gemm_plan_for_stride(const GemmPlan& p, int M, const int* Ns, int nproj, int64_t ldx,
+                              int K, bool int4);
 // int4: packed-int4 weights (TILE16X128_I4) take the large-tile rules only.
 GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
                    bool int4 = false);

@@ -21,7 +21,8 @@
 // src/ops/rpu_linear.cpp:664-731) with the fp16 per-channel scale carried
 // next to the int8 weight as in `causal_decoder_set_lm_head`
 // (registrations :46): input [..., K] is flattened to [M, K]
-// (rpu_linear.cpp:596-613), weight is int8 in the packed layout, scale fp16
+// (rpu_linear.cpp:596-613), weight is int8 in the packed layout (3-D tiles
+// [ceil(N/16), ceil(K/64), 1024]: a row-major [N, K] is refused), scale fp16
 // [N], bias fp16 [N] added once after the reduction.  Invalid input raises;
 // there is no CPU compute path and no silent fallback (the reference also
 // refuses to run swizzled weights on the CPU, rpu_linear.cpp:193-196).
@@ -44,8 +45,27 @@ void check_status(int st, const char* what) {
 }
 
 int64_t ceil_to(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Symbolic sizes (FakeTensor tracing with dynamic shapes) round the same way.
-c10::SymInt ceil_to(const c10::SymInt& a, int64_t b) { return (a + (b - 1)) / b * b; }
+c10::SymInt ceil_div(const c10::SymInt& a, int64_t b) { return (a + (b - 1)) / b; }
+
+// Packed weight shapes: [tiles along N, tiles along K, 1024 bytes].
+std::vector<int64_t> packed_sizes_int8(int64_t N, int64_t K) {
+  return {ceil_div(N, 16), ceil_div(K, 64), 1024};
+}
+std::vector<int64_t> packed_sizes_int4(int64_t N, int64_t K) {
+  return {ceil_div(N, 16), ceil_div(K, 128), 1024};
+}
+
+// Refuses anything but the packed tiles of an [N, K] weight (by rank and
+// sizes: a row-major or reference-packed 2-D matrix is never accepted).
+void check_packed(const at::Tensor& packed, at::ScalarType dtype,
+                  const std::vector<int64_t>& want, const char* op) {
+  TORCH_CHECK(packed.scalar_type() == dtype, op, ": packed must be ", dtype, ", got ",
+              packed.scalar_type());
+  TORCH_CHECK(packed.sizes() == at::IntArrayRef(want), op, ": packed must have shape ", want,
+              ", got ", packed.sizes());
+}
 
 // Workspace per (device, stream): allocated through torch's caching
 // allocator, zero-filled once (fill kernel), at least kMinWorkspace bytes.
@@ -140,10 +160,15 @@ std::pair<c10::SymInt, c10::SymInt> check_shapes(const at::Tensor& input, const 
   const c10::SymInt K = input.sym_size(-1);
   TORCH_CHECK(N >= 1, op, ": N (weight_scale.numel()) must be >= 1");
   TORCH_CHECK(K >= 8 && K % 8 == 0, op, ": in_features K=", K, " is zero or not a multiple of 8");
-  TORCH_CHECK(weight.is_contiguous() && weight.dim() == 2 &&
-                  weight.sym_size(0) == ceil_to(N, 16) && weight.sym_size(1) == ceil_to(K, 64),
-              op, ": packed weight must be contiguous int8 [", ceil_to(N, 16), ", ",
-              ceil_to(K, 64), "] for N=", N, ", K=", K, " (use w8a16.pack_weight), got ",
+  // The packed form is 3-D (one 1024-byte tile per 16 channels and 64 input
+  // positions); a row-major [N, K] matrix never has that rank, so one passed
+  // in its place is refused here instead of being read as tiles.
+  TORCH_CHECK(weight.is_contiguous() && weight.dim() == 3 &&
+                  weight.sym_size(0) == ceil_div(N, 16) && weight.sym_size(1) == ceil_div(K, 64) &&
+                  weight.sym_size(2) == 1024,
+              op, ": weight must be the packed int8 tiles [", ceil_div(N, 16), ", ",
+              ceil_div(K, 64), ", 1024] of an [N=", N, ", K=", K,
+              "] weight (use w8a16.pack_weight on the row-major int8 weight), got ",
               weight.sym_sizes());
   if (bias.has_value() && bias->defined()) {
     const at::Tensor& b = *bias;
@@ -285,9 +310,18 @@ std::vector<at::Tensor> linear_multi_hip(const at::Tensor& input, at::TensorList
   return outs;
 }
 
-std::vector<at::Tensor> linear_multi_cpu(const at::Tensor&, at::TensorList, at::TensorList,
-                                         const c10::List<c10::optional<at::Tensor>>&, int64_t,
-                                         int64_t) {
+std::vector<at::Tensor> linear_multi_meta(const at::Tensor& input, at::TensorList weights,
+                                          at::TensorList scales,
+                                          const c10::List<c10::optional<at::Tensor>>& biases,
+                                          int64_t layout, int64_t kernel);
+
+// CPU tensors: the same argument checks as the device path (so a row-major
+// weight is named as such), then a refusal -- there is no CPU compute.
+std::vector<at::Tensor> linear_multi_cpu(const at::Tensor& input, at::TensorList weights,
+                                         at::TensorList scales,
+                                         const c10::List<c10::optional<at::Tensor>>& biases,
+                                         int64_t layout, int64_t kernel) {
+  linear_multi_meta(input, weights, scales, biases, layout, kernel);
   TORCH_CHECK(false, "w8a16::linear_multi: tensors are on the CPU; the W8A16 kernels run on a "
               "HIP device (gfx950) only and there is no CPU implementation");
 }
@@ -359,13 +393,13 @@ at::Tensor pack_weight_meta(const at::Tensor& q) {
   TORCH_CHECK(q.scalar_type() == at::kChar && q.dim() == 2 && q.sym_size(0) >= 1 &&
                   q.sym_size(1) >= 1,
               "w8a16::pack_weight: q must be a non-empty int8 [N, K] tensor");
-  return at::empty_symint({ceil_to(q.sym_size(0), 16), ceil_to(q.sym_size(1), 64)}, q.options());
+  return at::empty_symint({ceil_div(q.sym_size(0), 16), ceil_div(q.sym_size(1), 64), 1024},
+                          q.options());
 }
 
 at::Tensor unpack_weight_meta(const at::Tensor& packed, int64_t N, int64_t K) {
-  TORCH_CHECK(packed.scalar_type() == at::kChar && N >= 1 && K >= 1 &&
-                  packed.sym_numel() == ceil_to(N, 16) * ceil_to(K, 64),
-              "w8a16::unpack_weight: packed must be int8 with ceil16(N) * ceil64(K) bytes");
+  TORCH_CHECK(N >= 1 && K >= 1, "w8a16::unpack_weight: N and K must be >= 1");
+  check_packed(packed, at::kChar, packed_sizes_int8(N, K), "w8a16::unpack_weight");
   return at::empty({N, K}, packed.options());
 }
 
@@ -375,15 +409,18 @@ at::Tensor unpack_weight_meta(const at::Tensor& packed, int64_t N, int64_t K) {
               "and there is no CPU implementation");
 }
 
-at::Tensor linear_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                      const c10::optional<at::Tensor>&, int64_t, int64_t) {
+at::Tensor linear_cpu(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                      const c10::optional<at::Tensor>& bias, int64_t layout, int64_t) {
+  check_shapes(input, weight, scale, bias, layout, "w8a16::linear");
   no_cpu("w8a16::linear");
 }
 
-std::tuple<at::Tensor, at::Tensor> linear_argmax_cpu(const at::Tensor&, const at::Tensor&,
-                                                     const at::Tensor&,
-                                                     const c10::optional<at::Tensor>&, bool,
-                                                     int64_t) {
+std::tuple<at::Tensor, at::Tensor> linear_argmax_cpu(const at::Tensor& input,
+                                                     const at::Tensor& weight,
+                                                     const at::Tensor& scale,
+                                                     const c10::optional<at::Tensor>& bias, bool,
+                                                     int64_t layout) {
+  check_shapes(input, weight, scale, bias, layout, "w8a16::linear_argmax");
   no_cpu("w8a16::linear_argmax");
 }
 
@@ -429,8 +466,10 @@ std::tuple<at::Tensor, at::Tensor> linear_argmax_hip(const at::Tensor& input,
   return {index, logits};
 }
 
-void linear_into_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                     const c10::optional<at::Tensor>&, at::Tensor&, int64_t, int64_t) {
+void linear_into_cpu(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& scale,
+                     const c10::optional<at::Tensor>& bias, at::Tensor&, int64_t layout,
+                     int64_t) {
+  check_shapes(input, weight, scale, bias, layout, "w8a16::linear_into");
   no_cpu("w8a16::linear_into");
 }
 
@@ -443,7 +482,7 @@ at::Tensor pack_weight(const at::Tensor& q) {
   const int64_t N = q.size(0), K = q.size(1);
   TORCH_CHECK(N >= 1 && K >= 1, "w8a16::pack_weight: empty weight ", q.sizes());
   at::Tensor qc = q.contiguous();
-  at::Tensor out = at::empty({ceil_to(N, 16), ceil_to(K, 64)}, q.options());
+  at::Tensor out = at::empty(packed_sizes_int8(N, K), q.options());
   const size_t bytes = rf_w8a16_packed_bytes(N, K);
   TORCH_CHECK((size_t)out.numel() == bytes, "w8a16::pack_weight: size mismatch");
   if (q.is_cuda()) {
@@ -462,11 +501,8 @@ at::Tensor pack_weight(const at::Tensor& q) {
 
 // Inverse of pack_weight (host); returns a CPU int8 [N, K] tensor.
 at::Tensor unpack_weight(const at::Tensor& packed, int64_t N, int64_t K) {
-  TORCH_CHECK(packed.scalar_type() == at::kChar, "w8a16::unpack_weight: packed must be int8");
   TORCH_CHECK(N >= 1 && K >= 1, "w8a16::unpack_weight: N and K must be >= 1");
-  TORCH_CHECK(packed.numel() == (int64_t)rf_w8a16_packed_bytes(N, K),
-              "w8a16::unpack_weight: packed has ", packed.numel(), " bytes, expected ",
-              rf_w8a16_packed_bytes(N, K));
+  check_packed(packed, at::kChar, packed_sizes_int8(N, K), "w8a16::unpack_weight");
   at::Tensor p = packed.to(at::kCPU).contiguous();
   at::Tensor q = at::empty({N, K}, p.options());
   check_status(rf_w8a16_unpack_weight(p.data_ptr(), N, K, q.data_ptr<int8_t>(), K),
@@ -478,7 +514,7 @@ at::Tensor unpack_weight(const at::Tensor& packed, int64_t N, int64_t K) {
 // The reference's launcher takes a packed-int4 weight as a uint8 [N, K/2]
 // tensor and tells per-channel from group-wise by the scale's rank
 // (src/ops/rpu_linear.cpp:1211-1489); so does this op: weight uint8
-// TILE16X128_I4 [ceil16(N), ceil128(K)/2], scale fp16 [N] (per-channel) or
+// TILE16X128_I4 tiles [ceil(N/16), ceil(K/128), 1024], scale fp16 [N] (per-channel) or
 // [G, N] (group-wise, group_size = K / G in {32, 64, 128}).
 // W4A16 dtype / shape checks (no device checks), shared by the HIP and Meta
 // kernels: N, K and the group size (0 = per-channel scale [N]).
@@ -515,10 +551,13 @@ W4Shape w4_check_shapes(const at::Tensor& input, const at::Tensor& weight, const
               " is zero or not a multiple of 16, which packed int4 needs");
   TORCH_CHECK(r.K >= 64 && r.K % 64 == 0, op, ": in_features K=", r.K,
               " is zero or not a multiple of 64, which packed int4 needs");
-  TORCH_CHECK(weight.is_contiguous() && weight.dim() == 2 && weight.sym_size(0) == r.N &&
-                  weight.sym_size(1) == ceil_to(r.K, 128) / 2,
-              op, ": packed weight must be contiguous uint8 [", r.N, ", ", ceil_to(r.K, 128) / 2,
-              "] for N=", r.N, ", K=", r.K, " (use w4a16.pack_weight), got ", weight.sym_sizes());
+  // 3-D packed tiles, never the rank of the reference's nibble-packed [N, K/2].
+  TORCH_CHECK(weight.is_contiguous() && weight.dim() == 3 &&
+                  weight.sym_size(0) == ceil_div(r.N, 16) &&
+                  weight.sym_size(1) == ceil_div(r.K, 128) && weight.sym_size(2) == 1024,
+              op, ": weight must be the packed int4 tiles [", ceil_div(r.N, 16), ", ",
+              ceil_div(r.K, 128), ", 1024] of an [N=", r.N, ", K=", r.K,
+              "] weight (use w4a16.pack_weight), got ", weight.sym_sizes());
   if (bias.has_value() && bias->defined()) {
     const at::Tensor& b = *bias;
     TORCH_CHECK(b.scalar_type() == at::kHalf, op, ": bias must be float16");
@@ -565,8 +604,9 @@ at::Tensor w4_linear_hip(const at::Tensor& input, const at::Tensor& weight, cons
   return y;
 }
 
-at::Tensor w4_linear_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                         const c10::optional<at::Tensor>&, int64_t) {
+at::Tensor w4_linear_cpu(const at::Tensor& input, const at::Tensor& weight,
+                         const at::Tensor& scale, const c10::optional<at::Tensor>& bias, int64_t) {
+  w4_check_shapes(input, weight, scale, bias, "w4a16::linear");
   TORCH_CHECK(false, "w4a16::linear: tensors are on the CPU; the W4A16 kernels run on a HIP "
               "device (gfx950) only and there is no CPU implementation");
 }
@@ -581,14 +621,13 @@ at::Tensor w4_pack_weight_meta(const at::Tensor& q) {
   TORCH_CHECK(q.scalar_type() == at::kChar && q.dim() == 2 && q.sym_size(0) >= 1 &&
                   q.sym_size(1) >= 1,
               "w4a16::pack_weight: q must be a non-empty int8 [N, K] tensor");
-  return at::empty_symint({ceil_to(q.sym_size(0), 16), ceil_to(q.sym_size(1), 128) / 2},
+  return at::empty_symint({ceil_div(q.sym_size(0), 16), ceil_div(q.sym_size(1), 128), 1024},
                           q.options().dtype(at::kByte));
 }
 
 at::Tensor w4_unpack_weight_meta(const at::Tensor& packed, int64_t N, int64_t K) {
-  TORCH_CHECK(packed.scalar_type() == at::kByte && N >= 1 && K >= 1 &&
-                  packed.sym_numel() == ceil_to(N, 16) * ceil_to(K, 128) / 2,
-              "w4a16::unpack_weight: packed must be uint8 with ceil16(N) * ceil128(K) / 2 bytes");
+  TORCH_CHECK(N >= 1 && K >= 1, "w4a16::unpack_weight: N and K must be >= 1");
+  check_packed(packed, at::kByte, packed_sizes_int4(N, K), "w4a16::unpack_weight");
   return at::empty({N, K}, packed.options().dtype(at::kChar));
 }
 
@@ -602,7 +641,7 @@ at::Tensor w4_pack_weight(const at::Tensor& q) {
   const int64_t N = q.size(0), K = q.size(1);
   TORCH_CHECK(N >= 1 && K >= 1, "w4a16::pack_weight: empty weight ", q.sizes());
   at::Tensor qc = q.contiguous();
-  at::Tensor out = at::empty({ceil_to(N, 16), ceil_to(K, 128) / 2}, q.options().dtype(at::kByte));
+  at::Tensor out = at::empty(packed_sizes_int4(N, K), q.options().dtype(at::kByte));
   const size_t bytes = rf_w4a16_packed_bytes(N, K);
   TORCH_CHECK((size_t)out.numel() == bytes, "w4a16::pack_weight: size mismatch");
   if (q.is_cuda()) {
@@ -621,11 +660,8 @@ at::Tensor w4_pack_weight(const at::Tensor& q) {
 }
 
 at::Tensor w4_unpack_weight(const at::Tensor& packed, int64_t N, int64_t K) {
-  TORCH_CHECK(packed.scalar_type() == at::kByte, "w4a16::unpack_weight: packed must be uint8");
   TORCH_CHECK(N >= 1 && K >= 1, "w4a16::unpack_weight: N and K must be >= 1");
-  TORCH_CHECK(packed.numel() == (int64_t)rf_w4a16_packed_bytes(N, K),
-              "w4a16::unpack_weight: packed has ", packed.numel(), " bytes, expected ",
-              rf_w4a16_packed_bytes(N, K));
+  check_packed(packed, at::kByte, packed_sizes_int4(N, K), "w4a16::unpack_weight");
   at::Tensor p = packed.to(at::kCPU).contiguous();
   at::Tensor q = at::empty({N, K}, p.options().dtype(at::kChar));
   check_status(rf_w4a16_unpack_weight(p.data_ptr(), N, K, q.data_ptr<int8_t>(), K),

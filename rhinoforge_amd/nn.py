@@ -9,11 +9,22 @@ a ``weight`` buffer of shape ``packed_shape(N, K)`` and the layout tag in
 
 The packed bytes never leave the module under the checkpoint's name: its
 state dict holds ``weight`` as the row-major int8 ``[N, K]`` checkpoint form
-(quant/convert_qwen3.py:65-100), unpacked on save and packed on load.  For
-most shapes packed and row-major tensors have the same dtype and shape, so
-without this a ``state_dict()`` / ``load_state_dict()`` round trip or an HF
-``save_pretrained`` would silently mix the two layouts (the hazard the
-reference guards with its recorded layout, runtime/weights.py:28-49).
+(quant/convert_qwen3.py:65-100), unpacked on save and packed on load, so a
+``state_dict()`` / ``load_state_dict()`` round trip or an HF
+``save_pretrained`` never mixes the two layouts (the hazard the reference
+guards with its recorded layout, runtime/weights.py:28-49).  The packed
+buffer itself is 3-D (``[ceil(N/16), ceil(K/64), 1024]`` tiles), a shape no
+row-major weight has.  ``state_dict()`` unpacks on the weight's own device
+(a tile permutation in torch ops): it costs one extra copy of the int8
+weight in device memory while the dict is alive, and no host round trip.
+
+State-dict versions (``_version``, recorded by torch in the dict's
+metadata): 2 is the logical [N, K] form above.  A version-1 dict was written
+by an earlier build of these modules, which stored either the logical form
+or the packed bytes as a 2-D [ceil16(N), ceil64(K)] tensor; where the shape
+tells which, it loads, and where both forms have the same shape (N % 16 == 0
+and K % 64 == 0 for int8) it is refused rather than guessed.  A dict with no
+version metadata (a checkpoint read from disk) holds the logical form.
 """
 from __future__ import annotations
 
@@ -27,8 +38,11 @@ from .quant import quantize_linear_per_channel
 class _LogicalWeightStateDict:
     """State-dict hooks of the packed-weight modules: ``weight`` is saved as
     the logical int8 [N, K] tensor and packed again on load.  Subclasses give
-    ``_unpack()`` and ``_pack(q)`` and the valid value range."""
+    ``_unpack_here()`` (on the weight's device), ``_pack(q)``, the valid
+    value range and ``_v1_packed_shape`` (the 2-D shape of the packed bytes
+    version-1 dicts may hold, in the packed buffer's dtype)."""
 
+    _version = 2
     _qmin, _qmax = -128, 127
 
     def _save_to_state_dict(self, destination, prefix, keep_vars):
@@ -37,7 +51,24 @@ class _LogicalWeightStateDict:
             destination[prefix + "weight"] = torch.empty(
                 (self.out_features, self.in_features), dtype=torch.int8, device="meta")
         else:
-            destination[prefix + "weight"] = self._unpack().to(self.weight.device)
+            destination[prefix + "weight"] = self._unpack_here()
+
+    def _v1_weight(self, t, key, error_msgs):
+        """The packed buffer for a version-1 dict's ``weight`` (logical or
+        2-D packed bytes, told apart by shape), or None after an error."""
+        shape = tuple(t.shape)
+        logical = t.dtype == torch.int8 and shape == (self.out_features, self.in_features)
+        packed = t.dtype == self.weight.dtype and shape == self._v1_packed_shape()
+        if logical and packed:
+            error_msgs.append(
+                f"{key}: a version-1 state dict (an earlier build of {type(self).__name__}) "
+                f"whose {list(shape)} weight may hold either the row-major checkpoint form or "
+                f"packed bytes; re-export it from that build with rowmajor_weight(), or load "
+                f"the row-major weight without the dict's version metadata")
+            return None
+        if packed:
+            return t.to(self.weight.device).reshape(self.weight.shape).contiguous()
+        return t  # the logical form (its checks follow)
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):
@@ -45,6 +76,19 @@ class _LogicalWeightStateDict:
         logical = state_dict.get(key)
         if logical is not None:
             want = (self.out_features, self.in_features)
+            version = local_metadata.get("version") if local_metadata else None
+            if version is not None and version < 2 and isinstance(logical, torch.Tensor):
+                got = self._v1_weight(logical, key, error_msgs)
+                if got is None:
+                    return
+                if got is not logical:  # packed bytes: installed as they are
+                    state_dict[key] = got
+                    try:
+                        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict,
+                                                      missing_keys, unexpected_keys, error_msgs)
+                    finally:
+                        state_dict[key] = logical
+                    return
             if logical.dtype != torch.int8 or tuple(logical.shape) != want:
                 error_msgs.append(
                     f"{key}: expected the logical int8 {list(want)} weight (the checkpoint "
@@ -74,8 +118,8 @@ class W8A16Linear(_LogicalWeightStateDict, nn.Module):
         self.in_features = in_features
         self.out_features = out_features
         self.layout = ops.LAYOUT_TILE16X64
-        np_, kp = ops.packed_shape(out_features, in_features)
-        self.register_buffer("weight", torch.full((np_, kp), -128, dtype=torch.int8, device=device))
+        self.register_buffer("weight", torch.full(ops.packed_shape(out_features, in_features),
+                                                  -128, dtype=torch.int8, device=device))
         self.register_buffer("weight_scale", torch.ones(out_features, dtype=torch.float16,
                                                         device=device))
         if bias:
@@ -120,7 +164,11 @@ class W8A16Linear(_LogicalWeightStateDict, nn.Module):
         """The int8 [N, K] row-major weight (CPU), e.g. for checkpoint export."""
         return ops.unpack_weight(self.weight, self.out_features, self.in_features)
 
-    _unpack = rowmajor_weight
+    def _unpack_here(self) -> torch.Tensor:
+        return ops.unpack_weight_on_device(self.weight, self.out_features, self.in_features)
+
+    def _v1_packed_shape(self) -> tuple[int, int]:
+        return ((self.out_features + 15) // 16 * 16, (self.in_features + 63) // 64 * 64)
 
     def _pack(self, q: torch.Tensor) -> torch.Tensor:
         return ops.pack_weight(q)
@@ -219,7 +267,12 @@ class W4A16Linear(_LogicalWeightStateDict, nn.Module):
         """The int4 values as an int8 [N, K] tensor (CPU)."""
         return ops.unpack_weight_int4(self.weight, self.out_features, self.in_features)
 
-    _unpack = rowmajor_weight
+    def _unpack_here(self) -> torch.Tensor:
+        return ops.unpack_weight_int4_on_device(self.weight, self.out_features,
+                                                self.in_features)
+
+    def _v1_packed_shape(self) -> tuple[int, int]:
+        return (self.out_features, (self.in_features + 127) // 128 * 64)
 
     def _pack(self, q: torch.Tensor) -> torch.Tensor:
         return ops.pack_weight_int4(q)

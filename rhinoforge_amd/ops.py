@@ -18,13 +18,16 @@ KERNEL_GEMV = 1
 KERNEL_GEMM = 2
 
 
-def packed_shape(n: int, k: int) -> tuple[int, int]:
-    """Shape of the packed int8 weight for a logical [n, k] weight."""
-    return ((n + 15) // 16 * 16, (k + 63) // 64 * 64)
+def packed_shape(n: int, k: int) -> tuple[int, int, int]:
+    """Shape of the packed int8 weight for a logical [n, k] weight: one
+    1024-byte tile per 16 output channels and 64 input channels,
+    ``[ceil(n/16), ceil(k/64), 1024]``.  A row-major ``[N, K]`` matrix never
+    has this rank, so the ops refuse one passed in its place."""
+    return ((n + 15) // 16, (k + 63) // 64, 1024)
 
 
 def pack_weight(q: torch.Tensor) -> torch.Tensor:
-    """Row-major int8 [N, K] -> TILE16X64 packed int8 [ceil16(N), ceil64(K)].
+    """Row-major int8 [N, K] -> TILE16X64 packed int8 ``packed_shape(N, K)``.
 
     Replaces the reference's load-time swizzle ``transform_linear_weight``
     (runtime/weights.py:206-233).  Runs on the device for HIP tensors and on
@@ -36,6 +39,23 @@ def pack_weight(q: torch.Tensor) -> torch.Tensor:
 def unpack_weight(packed: torch.Tensor, n: int, k: int) -> torch.Tensor:
     """Inverse of :func:`pack_weight`; returns a CPU int8 [n, k] tensor."""
     return torch.ops.w8a16.unpack_weight(packed, n, k)
+
+
+def unpack_weight_on_device(packed: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """:func:`unpack_weight` on the packed tensor's own device (a tile
+    permutation in torch ops, no host copy): the row-major int8 [n, k].
+
+    Byte j of lane l in tile (nb, kb) holds q[16 nb + l % 16][64 kb + 16 (l / 16) + j]
+    XOR 0x80, so the tiles viewed as [nb, kb, l / 16, l % 16, j] and permuted to
+    [nb, l % 16, kb, l / 16, j] are the padded row-major matrix."""
+    shape = packed_shape(n, k)
+    if packed.dtype != torch.int8 or tuple(packed.shape) != shape:
+        raise ValueError(f"packed must be int8 {list(shape)} for n={n}, k={k}, got "
+                         f"{packed.dtype} {list(packed.shape)}")
+    nb, kb, _ = shape
+    t = packed.view(torch.uint8).view(nb, kb, 4, 16, 16).permute(0, 3, 1, 2, 4)
+    t = t.reshape(nb * 16, kb * 64)[:n, :k] ^ 0x80
+    return t.contiguous().view(torch.int8)
 
 
 def linear(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
@@ -100,14 +120,17 @@ def select_kernel(m: int, n: int, k: int) -> int:
 LAYOUT_TILE16X128_I4 = 2
 
 
-def packed_shape_int4(n: int, k: int) -> tuple[int, int]:
-    """Shape of the packed uint8 int4 weight for a logical [n, k] weight."""
-    return ((n + 15) // 16 * 16, (k + 127) // 128 * 64)
+def packed_shape_int4(n: int, k: int) -> tuple[int, int, int]:
+    """Shape of the packed uint8 int4 weight for a logical [n, k] weight: one
+    1024-byte tile per 16 output channels and 128 input channels,
+    ``[ceil(n/16), ceil(k/128), 1024]`` (never the rank of the reference's
+    row-major nibble-packed ``[N, K/2]``)."""
+    return ((n + 15) // 16, (k + 127) // 128, 1024)
 
 
 def pack_weight_int4(q: torch.Tensor) -> torch.Tensor:
     """int4 values in int8 containers [N, K] (range [-8, 7]) -> TILE16X128_I4
-    packed uint8 [ceil16(N), ceil128(K)/2].
+    packed uint8 ``packed_shape_int4(N, K)``.
 
     Replaces the reference's nibble packers (quant/int4_pack.py:45-58,
     quant/int4_pgrp_pack.py:158-162) with one layout for both scale modes.
@@ -120,6 +143,28 @@ def pack_weight_int4(q: torch.Tensor) -> torch.Tensor:
 def unpack_weight_int4(packed: torch.Tensor, n: int, k: int) -> torch.Tensor:
     """Inverse of :func:`pack_weight_int4`; returns a CPU int8 [n, k] tensor."""
     return torch.ops.w4a16.unpack_weight(packed, n, k)
+
+
+def unpack_weight_int4_on_device(packed: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """:func:`unpack_weight_int4` on the packed tensor's own device, in torch ops.
+
+    Lane l of tile (nb, kt) holds channel 16 nb + l % 16, positions
+    128 kt + 32 (l / 16) + 8 w + i in dword w; inside a dword, position i sits
+    in nibble i / 2 (i even) or 4 + i / 2 (i odd), as q + 8.  Little-endian
+    bytes 0, 1 therefore carry positions 0, 2 | 4, 6 (low nibble first) and
+    bytes 2, 3 positions 1, 3 | 5, 7."""
+    shape = packed_shape_int4(n, k)
+    if packed.dtype != torch.uint8 or tuple(packed.shape) != shape:
+        raise ValueError(f"packed must be uint8 {list(shape)} for n={n}, k={k}, got "
+                         f"{packed.dtype} {list(packed.shape)}")
+    nb, kt, _ = shape
+    b = packed.view(nb, kt, 4, 16, 4, 4)           # [nb, kt, l/16, l%16, dword, byte]
+    nib = torch.stack((b & 0xF, b >> 4), dim=-1)    # [..., byte, lo/hi]
+    even = nib[..., 0:2, :].reshape(nb, kt, 4, 16, 4, 4)   # positions 0, 2, 4, 6
+    odd = nib[..., 2:4, :].reshape(nb, kt, 4, 16, 4, 4)    # positions 1, 3, 5, 7
+    pos = torch.stack((even, odd), dim=-1).reshape(nb, kt, 4, 16, 32)
+    q = pos.permute(0, 3, 1, 2, 4).reshape(nb * 16, kt * 128)[:n, :k]
+    return (q.to(torch.int16) - 8).to(torch.int8).contiguous()
 
 
 def linear_w4a16(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,

@@ -84,6 +84,11 @@ static void plans() {
                 CHECK(st == RF_W8A16_EINVAL);
                 continue;
               }
+              // int4 packing needs N % 16 == 0 and K % 64 == 0 (rf_w4a16_linear)
+              if (fmt != RF_W8A16_FORMAT_INT8 && (set[0] % 16 != 0 || K % 64 != 0)) {
+                CHECK(st == RF_W8A16_EINVAL);
+                continue;
+              }
               if (kernel == RF_W8A16_KERNEL_GEMV && M > 64) {
                 CHECK(st == RF_W8A16_EKERNEL);
                 continue;
@@ -99,6 +104,43 @@ static void plans() {
             }
       }
   CHECK(checked > 1000);
+  // the compute entry points' other refusals and fallbacks, at ldx = K
+  {
+    rf_w8a16_plan_info info;
+    const int64_t n64 = 64;
+    // GEMV offsets over 16 rows of x overflow 32 bits: AUTO plans the GEMM,
+    // a forced GEMV is refused
+    const int64_t kgemv = (int64_t)1 << 28;  // 15 rows * 2^28 * 2 bytes > 2^32
+    CHECK(rf_w8a16_plan(16, &n64, 1, kgemv, RF_W8A16_KERNEL_AUTO, RF_W8A16_FORMAT_INT8, 256, &info) ==
+          RF_W8A16_OK);
+    CHECK(info.kernel == RF_W8A16_KERNEL_GEMM);
+    CHECK(rf_w8a16_plan(16, &n64, 1, kgemv, RF_W8A16_KERNEL_GEMV, RF_W8A16_FORMAT_INT8, 256, &info) ==
+          RF_W8A16_EKERNEL);
+    // ... which fits at M = 1 (no row offsets) and at M = 16 with K = 2^27
+    CHECK(rf_w8a16_plan(1, &n64, 1, kgemv, RF_W8A16_KERNEL_AUTO, RF_W8A16_FORMAT_INT8, 256, &info) ==
+          RF_W8A16_OK);
+    CHECK(info.kernel == RF_W8A16_KERNEL_GEMV);
+    const int64_t kbig = (int64_t)1 << 27;
+    CHECK(rf_w8a16_plan(16, &n64, 1, kbig, RF_W8A16_KERNEL_AUTO, RF_W8A16_FORMAT_INT8, 256, &info) ==
+          RF_W8A16_OK);
+    CHECK(info.kernel == RF_W8A16_KERNEL_GEMV);
+    // int8 GEMM tile offsets overflow (128 rows * 2^27 * 2 bytes): the
+    // 64-bit-address kernel, unsplit
+    CHECK(rf_w8a16_plan(2048, &n64, 1, kbig, RF_W8A16_KERNEL_GEMM, RF_W8A16_FORMAT_INT8, 256, &info) ==
+          RF_W8A16_OK);
+    CHECK(std::strstr(info.name, "64-bit") != nullptr && info.splits == 1);
+    // int4 has no such kernel: refused
+    CHECK(rf_w8a16_plan(2048, &n64, 1, kbig, RF_W8A16_KERNEL_GEMM, RF_W8A16_FORMAT_INT4, 256, &info) ==
+          RF_W8A16_EKERNEL);
+    // int8 K % 8 != 0: EALIGN, as rf_w8a16_linear; int4 N % 16 / K % 64: EINVAL
+    CHECK(rf_w8a16_plan(1, &n64, 1, 100, RF_W8A16_KERNEL_AUTO, RF_W8A16_FORMAT_INT8, 256, &info) ==
+          RF_W8A16_EALIGN);
+    const int64_t n40 = 40;
+    CHECK(rf_w8a16_plan(1, &n40, 1, 128, RF_W8A16_KERNEL_AUTO, RF_W8A16_FORMAT_INT4, 256, &info) ==
+          RF_W8A16_EINVAL);
+    CHECK(rf_w8a16_plan(1, &n64, 1, 96, RF_W8A16_KERNEL_AUTO, RF_W8A16_FORMAT_INT4_GROUP, 256, &info) ==
+          RF_W8A16_EINVAL);
+  }
   // refusals
   rf_w8a16_plan_info info;
   const int64_t n1 = 64, n0 = 0;

@@ -613,7 +613,23 @@ def test_gpu_quantizer_matches_oracle():
 def test_device_pack_equals_host_pack():
     for n, k in [(17, 72), (3072, 1024), (100, 8)]:
         q = torch.randint(-128, 128, (n, k), dtype=torch.int8)
-        assert torch.equal(rf.pack_weight(q.to(DEV)).cpu(), rf.pack_weight(q))
+        packed = rf.pack_weight(q.to(DEV))
+        assert torch.equal(packed.cpu(), rf.pack_weight(q))
+        # the inverse on the device (what state_dict() uses) and on the host
+        back = rf.ops.unpack_weight_on_device(packed, n, k)
+        assert back.device == packed.device and torch.equal(back.cpu(), q)
+        assert torch.equal(rf.unpack_weight(packed, n, k), q)
+
+
+def test_module_state_dict_on_device_is_row_major():
+    q = torch.randint(-128, 128, (96, 320), dtype=torch.int8)
+    s = (torch.rand(96) * 0.01 + 1e-3).half()
+    mod = rf.W8A16Linear.from_quantized(q, s, device=DEV)
+    sd = mod.state_dict()
+    assert sd["weight"].device == mod.weight.device and torch.equal(sd["weight"].cpu(), q)
+    fresh = rf.W8A16Linear(320, 96, device=DEV)
+    fresh.load_state_dict(sd)
+    assert torch.equal(fresh.weight, mod.weight)
 
 
 def test_input_views_3d_empty_and_linear_into():
@@ -636,12 +652,18 @@ def test_input_views_3d_empty_and_linear_into():
 
 
 def test_op_errors_on_device():
-    # N=40, K=120: the row-major weight [40, 120] differs in shape from the
-    # packed one [48, 128], so passing it unpacked must be refused.
+    # A row-major weight is refused, whatever its shape: the packed form is
+    # the 3-D tiles [ceil(N/16), ceil(K/64), 1024].
     x, q, s, _ = make_case(2, 40, 120, seed=14)
     packed, sd = rf.pack_weight(_to_dev(q)), _to_dev(s)
-    with pytest.raises(RuntimeError, match="packed weight"):
+    with pytest.raises(RuntimeError, match="packed int8 tiles"):
         rf.linear(_to_dev(x), _to_dev(q), sd)  # row-major weight, not packed
+    x2, q2, s2, _ = make_case(2, 64, 128, seed=15)   # row-major [64, 128]: aligned shape
+    for call in (lambda w: rf.linear(_to_dev(x2), w, _to_dev(s2)),
+                 lambda w: rf.linear_multi(_to_dev(x2), [w], [_to_dev(s2)]),
+                 lambda w: rf.linear_argmax(_to_dev(x2), w, _to_dev(s2))):
+        with pytest.raises(RuntimeError, match="packed int8 tiles"):
+            call(_to_dev(q2))
     with pytest.raises(RuntimeError, match="GEMV|cannot run"):
         rf.linear(torch.zeros(65, 120, dtype=torch.float16, device=DEV), packed, sd,
                   kernel=rf.KERNEL_GEMV)

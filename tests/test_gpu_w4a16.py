@@ -65,8 +65,10 @@ def check(y, x, q, s, b=None, label="", rows=None):
 def test_device_pack_matches_host(n, k):
     q = np.random.default_rng(n + k).integers(-8, 8, (n, k)).astype(np.int8)
     host = rf.pack_weight_int4(torch.from_numpy(q))
-    dev = rf.pack_weight_int4(_dev(q)).cpu()
-    assert torch.equal(host, dev)
+    packed = rf.pack_weight_int4(_dev(q))
+    assert torch.equal(host, packed.cpu())
+    back = rf.ops.unpack_weight_int4_on_device(packed, n, k)   # state_dict()'s inverse
+    assert back.device == packed.device and np.array_equal(back.cpu().numpy(), q)
 
 
 @pytest.mark.parametrize("gs", [0, 32, 128])
@@ -160,7 +162,7 @@ def test_w4a16_linear_module_and_errors():
         rf.linear_w4a16(x, w, torch.ones(24, dtype=torch.float16, device=DEV))
     with pytest.raises(RuntimeError, match="uint8"):
         rf.linear_w4a16(x, w.to(torch.int8), torch.ones(32, dtype=torch.float16, device=DEV))
-    with pytest.raises(RuntimeError, match="packed weight"):
+    with pytest.raises(RuntimeError, match="packed int4 tiles"):
         rf.linear_w4a16(torch.zeros(2, 256, dtype=torch.float16, device=DEV), w,
                         torch.ones(32, dtype=torch.float16, device=DEV))
 

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(capi.LIB_PATH))
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert capi.load().rf_w8a16_abi_version() == 3
+    assert capi.load().rf_w8a16_abi_version() == 4
 
 
 def test_status_strings():
@@ -65,9 +65,8 @@ def test_pack_matches_layout_definition_and_round_trips(n, k):
     rng = np.random.default_rng(n * 1000 + k)
     q = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
     packed = rf.pack_weight(torch.from_numpy(q)).numpy().view(np.uint8).ravel()
-    np_, kp = rf.packed_shape(n, k)
-    assert packed.size == np_ * kp
-    kblocks = kp // 64
+    nb, kblocks, tile = rf.packed_shape(n, k)
+    assert tile == 1024 and packed.size == nb * kblocks * 1024
     # every logical element lands where the header says, stored as q XOR 0x80
     idx = np.array([[_layout_index(i, j, kblocks) for j in range(k)] for i in range(n)])
     assert (packed[idx] == (q.view(np.uint8) ^ 0x80)).all()
@@ -76,8 +75,10 @@ def test_pack_matches_layout_definition_and_round_trips(n, k):
     mask[idx.ravel()] = False
     assert (packed[mask] == 0x80).all()
     # inverse
-    assert (rf.unpack_weight(torch.from_numpy(packed.view(np.int8).reshape(np_, kp)), n, k).numpy()
-            == q).all()
+    packed_t = torch.from_numpy(packed.view(np.int8).reshape(nb, kblocks, 1024))
+    assert (rf.unpack_weight(packed_t, n, k).numpy() == q).all()
+    # the torch-op form of the inverse (used by state_dict on the weight's device)
+    assert (rf.ops.unpack_weight_on_device(packed_t, n, k).numpy() == q).all()
 
 
 def test_pack_is_a_permutation_on_aligned_shapes():
@@ -220,7 +221,7 @@ def test_torch_op_schemas_registered():
 
 def test_torch_op_meta_shape():
     x = torch.empty(2, 3, 1024, dtype=torch.float16, device="meta")
-    w = torch.empty(3072, 1024, dtype=torch.int8, device="meta")
+    w = torch.empty(rf.packed_shape(3072, 1024), dtype=torch.int8, device="meta")
     s = torch.empty(3072, dtype=torch.float16, device="meta")
     assert rf.linear(x, w, s).shape == (2, 3, 3072)
 

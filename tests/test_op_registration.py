@@ -43,10 +43,10 @@ def _cases():
         "w8a16::pack_weight": (w8.pack_weight.default, (q,)),
         "w8a16::unpack_weight": (w8.unpack_weight.default, (w8.pack_weight(q), 40, 70)),
         "w4a16::linear group-wise": (w4.linear.default,
-                                     (_meta((3, 128), torch.float16), _meta((48, 64), torch.uint8),
+                                     (_meta((3, 128), torch.float16), _meta(rf.packed_shape_int4(48, 128), torch.uint8),
                                       _meta((4, 48), torch.float16))),
         "w4a16::linear per-channel": (w4.linear.default,
-                                      (_meta((3, 128), torch.float16), _meta((48, 64), torch.uint8),
+                                      (_meta((3, 128), torch.float16), _meta(rf.packed_shape_int4(48, 128), torch.uint8),
                                        _meta((48,), torch.float16))),
         "w4a16::pack_weight": (w4.pack_weight.default, (q4,)),
         "w4a16::unpack_weight": (w4.unpack_weight.default, (w4.pack_weight(q4), 48, 128)),
@@ -73,7 +73,7 @@ def test_every_schema_is_covered():
 def test_meta_kernels_check_shapes_like_the_device_kernels():
     x = _meta((M, K), torch.float16)
     s = _meta((N,), torch.float16)
-    with pytest.raises(RuntimeError, match="packed weight must be contiguous int8"):
+    with pytest.raises(RuntimeError, match="packed int8 tiles"):
         torch.ops.w8a16.linear(x, _meta((N, K), torch.int8), s)  # unpacked (row-major) shape
     w = _meta(rf.packed_shape(N, K), torch.int8)
     with pytest.raises(RuntimeError, match="input must be float16"):
@@ -83,7 +83,7 @@ def test_meta_kernels_check_shapes_like_the_device_kernels():
     with pytest.raises(RuntimeError, match="out shape"):
         torch.ops.w8a16.linear_into(x, w, s, None, _meta((M, N + 1), torch.float16))
     with pytest.raises(RuntimeError, match="32, 64 or 128"):
-        torch.ops.w4a16.linear(_meta((3, 128), torch.float16), _meta((48, 64), torch.uint8),
+        torch.ops.w4a16.linear(_meta((3, 128), torch.float16), _meta(rf.packed_shape_int4(48, 128), torch.uint8),
                                _meta((8, 48), torch.float16))
 
 
@@ -97,3 +97,41 @@ def test_outputs_do_not_require_grad():
     assert y.shape == (M, N) and not y.requires_grad
     ys = torch.ops.w8a16.linear_multi(x, [w], [s], [None])
     assert not ys[0].requires_grad
+
+
+def test_a_row_major_weight_is_refused_by_every_op():
+    """A row-major int8 [N, K] passed where the packed tiles belong raises in
+    every op, also where N % 16 == 0 and K % 64 == 0 (every Qwen3 projection),
+    on meta tensors and on CPU tensors alike: the packed form is 3-D
+    [ceil(N/16), ceil(K/64), 1024], a rank no row-major weight has."""
+    w8, w4 = torch.ops.w8a16, torch.ops.w4a16
+    for dev in ("meta", "cpu"):
+        x = torch.zeros(2, 4096, dtype=torch.float16, device=dev)
+        q = torch.zeros(4096, 4096, dtype=torch.int8, device=dev)      # row-major [N, K]
+        s = torch.ones(4096, dtype=torch.float16, device=dev)
+        flat = torch.zeros(4096 * 4096, dtype=torch.int8, device=dev)  # right bytes, wrong shape
+        out = torch.empty(2, 4096, dtype=torch.float16, device=dev)
+        calls = {
+            "linear": lambda w: w8.linear(x, w, s),
+            "linear_into": lambda w: w8.linear_into(x, w, s, None, out),
+            "linear_multi": lambda w: w8.linear_multi(x, [w, w], [s, s], [None, None]),
+            "linear_argmax": lambda w: w8.linear_argmax(x, w, s, None, False),
+        }
+        for name, call in calls.items():
+            for w in (q, flat):
+                with pytest.raises(RuntimeError, match="packed int8 tiles"):
+                    call(w)
+        # the packed shape itself passes the checks (meta: shape inference;
+        # cpu: then refused only for having no CPU implementation)
+        wp = torch.zeros(rf.packed_shape(4096, 4096), dtype=torch.int8, device=dev)
+        if dev == "meta":
+            assert w8.linear(x, wp, s).shape == (2, 4096)
+        else:
+            with pytest.raises(RuntimeError, match="no CPU implementation"):
+                w8.linear(x, wp, s)
+        # int4: the reference's nibble-packed uint8 [N, K/2] is refused too
+        q4 = torch.zeros(4096, 2048, dtype=torch.uint8, device=dev)
+        with pytest.raises(RuntimeError, match="packed int4 tiles"):
+            w4.linear(x, q4, s)
+    with pytest.raises(RuntimeError, match="packed must have shape"):
+        rf.unpack_weight(torch.zeros(4096, 4096, dtype=torch.int8), 4096, 4096)

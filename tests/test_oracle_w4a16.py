@@ -210,7 +210,8 @@ def test_w4a16_op_schema_and_cpu_refusal():
     with pytest.raises(RuntimeError, match="no CPU implementation"):
         m(torch.zeros(1, 128, dtype=torch.float16))
     x = torch.empty(3, 128, dtype=torch.float16, device="meta")
-    out = torch.ops.w4a16.linear(x, torch.empty(32, 64, dtype=torch.uint8, device="meta"),
+    out = torch.ops.w4a16.linear(x, torch.empty(rf.packed_shape_int4(32, 128), dtype=torch.uint8,
+                                                device="meta"),
                                  torch.empty(32, dtype=torch.float16, device="meta"), None, 0)
     assert out.shape == (3, 32)
 

@@ -62,13 +62,15 @@ def _run(entry, x, ws, kernel):
     return st, outs
 
 
-# (first call, second smaller call): (M, output widths, K, kernel)
+# (first call, second smaller call): (M, output widths, K, kernel).  Every
+# call's plan splits K, so every call uses the scratch (asserted below).
 SEQUENCES = [
     # GEMV: M=16, K=12288 takes a 4-way K split; then M=4, one 1024-wide weight
-    # (64 strips: 4-way split)
-    ((16, [1024, 512, 256], 12288, capi.KERNEL_AUTO), (4, [1024], 4096, capi.KERNEL_AUTO)),
-    # GEMM: M=512 k/v-like (64 tiles of 128x128: two K groups, K split) then M=300, one weight
-    ((512, [1024, 1024], 5120, capi.KERNEL_AUTO), (300, [512], 2048, capi.KERNEL_GEMM)),
+    # with K=16384 (64 strips, 256 K blocks: 8-way split)
+    ((16, [1024, 512, 256], 12288, capi.KERNEL_AUTO), (4, [1024], 16384, capi.KERNEL_AUTO)),
+    # GEMM: M=512 k/v-like (64 tiles of 128x128: two K groups, 4-way K split)
+    # then M=128, one weight (64x64 tiles, two K groups, 4-way split)
+    ((512, [1024, 1024], 5120, capi.KERNEL_AUTO), (128, [1024], 4096, capi.KERNEL_GEMM)),
     # the mid-M GEMM tiles (M <= 64, K split to ~3 workgroups per CU), forced
     ((40, [2048, 1024], 4096, capi.KERNEL_GEMM), (24, [1024], 2048, capi.KERNEL_GEMM)),
 ]
@@ -78,6 +80,8 @@ SEQUENCES = [
 def test_noalloc_matches_workspace_entry_point(seq):
     for call, (m, ns, k, kernel) in enumerate(SEQUENCES[seq]):
         _say(f"noalloc seq {seq} call {call}: M={m} Ns={ns} K={k} kernel={kernel}")
+        plan = capi.plan(m, ns, k, kernel=kernel)
+        assert plan["splits"] > 1 and plan["workspace_bytes"] > 0, plan  # uses the scratch
         x, ws = _case(m, ns, k, seed=100 * seq + call)
         st, ref = _run("workspace", x, ws, kernel)
         capi.check(st, "rf_w8a16_linear_multi")
@@ -119,3 +123,82 @@ def test_noalloc_refuses_shapes_beyond_its_scratch():
     assert st == capi.ESCRATCH, capi.status_str(st)
     assert torch.isnan(y).all()  # nothing ran
     assert "noalloc" in capi.status_str(st)
+
+
+# Run in a fresh interpreter, so that the captured call below is the first
+# no-allocation call of the process (the one that looks up the scratch array).
+_CAPTURED_FIRST_CALL = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+import rhinoforge_amd as rf
+from rhinoforge_amd import capi
+from oracle import w8a16 as o
+
+m, ns, k = 4, [1024], 16384                 # GEMV with an 8-way K split
+assert capi.plan(m, ns, k)["splits"] > 1
+lib = capi.load()
+x = torch.from_numpy(o.make_activation(7, m, k)).cuda()
+q, s = o.quantize_linear_per_channel(o.make_weight(8, ns[0], k))
+wp, sd = rf.pack_weight(torch.from_numpy(q).cuda()), torch.from_numpy(s).cuda()
+ref = rf.linear(x, wp, sd)                  # the workspace path (torch op)
+y = torch.full((m, ns[0]), float("nan"), dtype=torch.float16, device="cuda")
+arr = (capi.Proj * 1)(capi.Proj(wp.data_ptr(), sd.data_ptr(), None, y.data_ptr(), ns[0], ns[0]))
+torch.cuda.synchronize()
+side = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+dump = hasattr(g, "enable_debug_mode")
+if dump:
+    g.enable_debug_mode()
+st = []
+with torch.cuda.graph(g, stream=side):
+    st.append(lib.rf_w8a16_linear_multi_noalloc(x.data_ptr(), k, capi.LAYOUT_TILE16X64, arr, 1,
+                                                m, k, capi.KERNEL_AUTO,
+                                                ctypes.c_void_p(side.cuda_stream)))
+capi.check(st[0], "captured first rf_w8a16_linear_multi_noalloc")
+torch.cuda.synchronize()
+assert torch.isnan(y).all()                 # captured, not run
+for rep in range(3):
+    y.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref), f"replay {rep}"
+    # eager no-allocation calls between replays share the counters
+    y2 = torch.full_like(y, float("nan"))
+    arr2 = (capi.Proj * 1)(capi.Proj(wp.data_ptr(), sd.data_ptr(), None, y2.data_ptr(), ns[0], ns[0]))
+    capi.check(lib.rf_w8a16_linear_multi_noalloc(x.data_ptr(), k, capi.LAYOUT_TILE16X64, arr2, 1,
+                                                 m, k, capi.KERNEL_AUTO,
+                                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+               "eager rf_w8a16_linear_multi_noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(y2, ref), f"eager call after replay {rep}"
+kernels = None
+if dump:
+    import os, tempfile
+    path = os.path.join(tempfile.mkdtemp(), "g.dot")
+    try:
+        g.debug_dump(path)
+        kernels = open(path).read()
+    except Exception as e:  # no graph dump on this build: the counter check above stands
+        print("no graph dump:", e)
+if kernels is not None:
+    assert "gemv" in kernels and "zero_u4" not in kernels, "the first-call fill was captured"
+print("captured first call ok", "(graph dump checked)" if kernels is not None else "")
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The first no-allocation call of a process made under HIP graph capture:
+    it records the GEMV (8-way K split) and no counter fill, so every replay,
+    with eager no-allocation calls in between, matches the workspace entry
+    point bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+    _say("noalloc: first call under graph capture (fresh process)")
+    res = subprocess.run([sys.executable, "-c", _CAPTURED_FIRST_CALL, root], capture_output=True,
+                         text=True, timeout=110)
+    _say(res.stdout[-2000:] + res.stderr[-2000:])
+    assert res.returncode == 0, res.stderr[-3000:]
+    assert "captured first call ok" in res.stdout
