@@ -601,6 +601,21 @@ def bench_w4a16(torch, rf):
             rows.append({"group_size": gs, "M": m, "proj": "layer (7 launches)",
                          "us": round(step_us, 2),
                          "GBps": round(step_bytes / (step_us * 1e-6) / 1e9, 1)})
+            # the layer as a decoder issues it: q/k/v and gate/up each in one
+            # w4a16.linear_multi launch (they share the input), o, down -- 4 launches
+
+            def layer4(c, x=x):
+                for idxs in DECODE_GROUPS:
+                    xx = x[:, :QWEN3_8B[idxs[0]][2]]
+                    if len(idxs) == 1:
+                        rf.linear_w4a16(xx, c[idxs[0]][3], c[idxs[0]][4])
+                    else:
+                        rf.linear_multi_w4a16(xx, [c[i][3] for i in idxs], [c[i][4] for i in idxs])
+            us4 = per_launch_us(torch, layer4, copies, 12)
+            # x is read once per launch
+            b4 = step_bytes - sum(2 * m * QWEN3_8B[g[0]][2] * (len(g) - 1) for g in DECODE_GROUPS)
+            rows.append({"group_size": gs, "M": m, "proj": "layer (4 launches: qkv, o, gate_up, down)",
+                         "us": round(us4, 2), "GBps": round(b4 / (us4 * 1e-6) / 1e9, 1)})
         if gs in (0, 32):
             x = torch.randn(PREFILL_M, 12288, device="cuda").half()
             for idx in (4, 6):  # gate (12288x4096) and down (4096x12288)

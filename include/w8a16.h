@@ -291,6 +291,8 @@ int rf_w4a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K, int64
                                 void* dst_dev, size_t dst_bytes, void* stream);
 /* Workspace a W4A16 call needs (counter region + split-K partials). */
 size_t rf_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
+/* Workspace of rf_w4a16_linear_multi for `count` projections of widths Ns. */
+size_t rf_w4a16_workspace_bytes_multi(int64_t M, const int64_t* Ns, int32_t count, int64_t K);
 /* y = x . W^T (+ b) with a TILE16X128_I4 weight.  group_size: 0 (per-channel
  * scale [N]) or 32 / 64 / 128 (scale [K/group_size][N], 16-byte aligned).
  * kernel, workspace and stream as for rf_w8a16_linear; the int4 GEMM has no
@@ -300,6 +302,18 @@ int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void
                     int32_t group_size, const void* bias, void* y, int64_t ldy, int64_t M,
                     int64_t N, int64_t K, int32_t kernel, void* workspace, size_t workspace_bytes,
                     void* stream);
+/* y_i = x . W_i^T (+ b_i) for i < count (1..RF_W8A16_MAX_PROJ) TILE16X128_I4
+ * weights sharing x [M, ldx], K and group_size, in ONE launch of the chosen
+ * kernel (q/k/v or gate/up of a decoder layer), as rf_w8a16_linear_multi
+ * does for int8.  projs[i].w_packed is the packed int4 weight and
+ * projs[i].scale its scale ([N_i], or [K/group_size][N_i], 16-byte aligned);
+ * every N_i % 16 == 0.  The reference has no fused int4 launcher: its
+ * packed-int4 branch (src/ops/rpu_linear.cpp:1211-1489) runs one weight per
+ * call; this is the int4 form of its fused Q/K/V W8A16 launcher
+ * (rpu_linear.cpp:1546-1674). */
+int rf_w4a16_linear_multi(const void* x, int64_t ldx, const rf_w8a16_proj* projs, int32_t count,
+                          int32_t group_size, int64_t M, int64_t K, int32_t kernel,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

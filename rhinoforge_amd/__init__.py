@@ -39,6 +39,7 @@ from .ops import (  # noqa: E402
     linear_argmax,
     linear_into,
     linear_multi,
+    linear_multi_w4a16,
     linear_w4a16,
     pack_weight,
     pack_weight_int4,
@@ -69,6 +70,7 @@ __all__ = [
     "linear_argmax",
     "linear_into",
     "linear_multi",
+    "linear_multi_w4a16",
     "linear_w4a16",
     "pack_weight",
     "pack_weight_int4",

@@ -91,6 +91,11 @@ SIGNATURES = {
     "rf_w4a16_pack_weight_device": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                                _c.c_void_p, _c.c_size_t, _c.c_void_p]),
     "rf_w4a16_workspace_bytes": (_c.c_size_t, [_c.c_int64, _c.c_int64, _c.c_int64]),
+    "rf_w4a16_workspace_bytes_multi": (_c.c_size_t, [_c.c_int64, _c.POINTER(_c.c_int64), _c.c_int32,
+                                                     _c.c_int64]),
+    "rf_w4a16_linear_multi": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.POINTER(Proj), _c.c_int32,
+                                         _c.c_int32, _c.c_int64, _c.c_int64, _c.c_int32,
+                                         _c.c_void_p, _c.c_size_t, _c.c_void_p]),
     "rf_w4a16_linear": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_void_p,
                                    _c.c_int32, _c.c_void_p, _c.c_void_p, _c.c_int64,
                                    _c.c_int64, _c.c_int64, _c.c_int64, _c.c_int32,

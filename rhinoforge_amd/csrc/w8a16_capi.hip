@@ -310,7 +310,6 @@ int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_
       format != RF_W8A16_FORMAT_INT4_GROUP)
     return RF_W8A16_EINVAL;
   const bool int4 = format != RF_W8A16_FORMAT_INT8;
-  if (int4 && count != 1) return RF_W8A16_EINVAL;  // int4 calls take one projection
   int n32[RF_W8A16_MAX_PROJ];
   int64_t ntotal = 0;
   for (int i = 0; i < count; ++i) {
@@ -342,7 +341,7 @@ int rf_w8a16_plan(int64_t M, const int64_t* Ns, int32_t count, int64_t K, int32_
   memset(out, 0, sizeof(*out));
   out->kernel = kernel;
   if (kernel == RF_W8A16_KERNEL_GEMV) {
-    const rf::GemvPlan p = int4 ? rf::plan_gemv_int4((int)M, n32[0], (int)K,
+    const rf::GemvPlan p = int4 ? rf::plan_gemv_int4((int)M, n32, count, (int)K,
                                                      format == RF_W8A16_FORMAT_INT4_GROUP, dev)
                                 : rf::plan_gemv((int)M, n32, count, (int)K, dev);
     int waves = 0;
@@ -575,39 +574,55 @@ int rf_w4a16_pack_weight_device(const int8_t* q_dev, int64_t N, int64_t K, int64
   return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
 }
 
-size_t rf_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK) return 0;
+size_t rf_w4a16_workspace_bytes_multi(int64_t M, const int64_t* Ns, int32_t count, int64_t K) {
+  if (!Ns || count < 1 || count > RF_W8A16_MAX_PROJ || M < 1 || M > kMaxDim) return 0;
+  int n32[RF_W8A16_MAX_PROJ];
+  for (int i = 0; i < count; ++i) {
+    if (check_nk(Ns[i], K) != RF_W8A16_OK) return 0;
+    n32[i] = (int)Ns[i];
+  }
   rf::DeviceInfo dev;
   if (rf::device_info(&dev) != RF_W8A16_OK) {
     dev.cus = 256;
     dev.gfx950 = false;
   }
-  const int n32 = (int)N;
-  size_t extra = rf::gemm_workspace_bytes(rf::plan_gemm((int)M, &n32, 1, (int)K, dev, true));
+  size_t extra = rf::gemm_workspace_bytes(rf::plan_gemm((int)M, n32, count, (int)K, dev, true));
   if (M <= 64) {
     // Either scale format: the plans may differ.
     for (const bool grouped : {false, true}) {
-      const rf::GemvPlan p = rf::plan_gemv_int4((int)M, n32, (int)K, grouped, dev);
-      const size_t g = rf::gemv_workspace_bytes(p, (int)M, &n32, 1);
+      const rf::GemvPlan p = rf::plan_gemv_int4((int)M, n32, count, (int)K, grouped, dev);
+      const size_t g = rf::gemv_workspace_bytes(p, (int)M, n32, count);
       extra = g > extra ? g : extra;
     }
   }
   return RF_W8A16_WS_COUNTER_BYTES + extra;
 }
 
-int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void* scale,
-                    int32_t group_size, const void* bias, void* y, int64_t ldy, int64_t M,
-                    int64_t N, int64_t K, int32_t kernel, void* workspace, size_t workspace_bytes,
-                    void* stream) {
-  if (!x || !w_packed || !scale || !y) return RF_W8A16_EINVAL;
-  if (M < 1 || M > kMaxDim || check_nk(N, K) != RF_W8A16_OK || ldx < K || ldy < N)
-    return RF_W8A16_EINVAL;
+size_t rf_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return rf_w4a16_workspace_bytes_multi(M, &N, 1, K);
+}
+
+int rf_w4a16_linear_multi(const void* x, int64_t ldx, const rf_w8a16_proj* projs, int32_t count,
+                          int32_t group_size, int64_t M, int64_t K, int32_t kernel,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (!x || !projs || count < 1 || count > RF_W8A16_MAX_PROJ) return RF_W8A16_EINVAL;
+  if (M < 1 || M > kMaxDim || K < 1 || K > kMaxDim || ldx < K) return RF_W8A16_EINVAL;
   if (group_size != 0 && group_size != 32 && group_size != 64 && group_size != 128)
     return RF_W8A16_EINVAL;
-  if (N % 16 != 0 || K % 64 != 0 || (group_size && K % group_size != 0)) return RF_W8A16_EINVAL;
-  if (ldx % 8 != 0 || !aligned(x, 16) || !aligned(w_packed, 16) ||
-      !aligned(scale, group_size ? 16 : 2) || !aligned(y, 2) || (bias && !aligned(bias, 2)))
-    return RF_W8A16_EALIGN;
+  if (K % 64 != 0 || (group_size && K % group_size != 0)) return RF_W8A16_EINVAL;
+  for (int i = 0; i < count; ++i) {
+    const rf_w8a16_proj& q = projs[i];
+    if (!q.w_packed || !q.scale || !q.y) return RF_W8A16_EINVAL;
+    if (check_nk(q.N, K) != RF_W8A16_OK || q.ldy < q.N || q.N % 16 != 0) return RF_W8A16_EINVAL;
+  }
+  if (ldx % 8 != 0 || !aligned(x, 16)) return RF_W8A16_EALIGN;
+  for (int i = 0; i < count; ++i) {
+    const rf_w8a16_proj& q = projs[i];
+    // group-wise scale rows are copied with 16-byte DMAs
+    if (!aligned(q.w_packed, 16) || !aligned(q.scale, group_size ? 16 : 2) || !aligned(q.y, 2) ||
+        (q.bias && !aligned(q.bias, 2)))
+      return RF_W8A16_EALIGN;
+  }
 
   rf::DeviceInfo dev;
   int st = rf::device_info(&dev);
@@ -629,35 +644,53 @@ int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void
   pr.ldx = ldx;
   pr.M = (int)M;
   pr.K = (int)K;
-  pr.nproj = 1;
+  pr.nproj = count;
   pr.wf = group_size ? rf::kWfInt4Grp : rf::kWfInt4;
   pr.gshift = group_size == 128 ? 2 : group_size == 64 ? 1 : 0;
-  rf::Projection& d = pr.proj[0];
-  d.w = static_cast<const uint8_t*>(w_packed);
-  d.scale = static_cast<const _Float16*>(scale);
-  d.bias = static_cast<const _Float16*>(bias);
-  d.y = static_cast<_Float16*>(y);
-  d.ldy = ldy;
-  d.N = (int)N;
-  const int n32 = d.N;
+  int n32[RF_W8A16_MAX_PROJ];
+  for (int i = 0; i < count; ++i) {
+    rf::Projection& d = pr.proj[i];
+    d.w = static_cast<const uint8_t*>(projs[i].w_packed);
+    d.scale = static_cast<const _Float16*>(projs[i].scale);
+    d.bias = static_cast<const _Float16*>(projs[i].bias);
+    d.y = static_cast<_Float16*>(projs[i].y);
+    d.ldy = projs[i].ldy;
+    d.N = (int)projs[i].N;
+    n32[i] = d.N;
+  }
   auto workspace_ok = [&](size_t extra) {
     return workspace && workspace_bytes >= RF_W8A16_WS_COUNTER_BYTES + extra &&
            aligned(workspace, 256);
   };
   hipError_t e;
   if (kernel == RF_W8A16_KERNEL_GEMV) {
-    const rf::GemvPlan p = rf::plan_gemv_int4(pr.M, n32, pr.K, group_size != 0, dev);
-    if (p.splits > 1 && !workspace_ok(rf::gemv_workspace_bytes(p, pr.M, &n32, 1)))
+    const rf::GemvPlan p = rf::plan_gemv_int4(pr.M, n32, count, pr.K, group_size != 0, dev);
+    if (p.splits > 1 && !workspace_ok(rf::gemv_workspace_bytes(p, pr.M, n32, count)))
       return RF_W8A16_EWORKSPACE;
     e = rf::launch_gemv(pr, p, p.splits > 1 ? workspace : nullptr, s);
   } else {
-    const rf::GemmPlan p = rf::plan_gemm(pr.M, &n32, 1, pr.K, dev, true);
+    const rf::GemmPlan p = rf::plan_gemm(pr.M, n32, count, pr.K, dev, true);
     // The int4 GEMM has no 64-bit-address kernel.
     if (!rf::gemm_offsets_fit(p, ldx, pr.K, true)) return RF_W8A16_EKERNEL;
     if (p.splits > 1 && !workspace_ok(rf::gemm_workspace_bytes(p))) return RF_W8A16_EWORKSPACE;
     e = rf::launch_gemm(pr, p, p.splits > 1 ? workspace : nullptr, s);
   }
   return e == hipSuccess ? RF_W8A16_OK : RF_W8A16_EHIP;
+}
+
+int rf_w4a16_linear(const void* x, int64_t ldx, const void* w_packed, const void* scale,
+                    int32_t group_size, const void* bias, void* y, int64_t ldy, int64_t M,
+                    int64_t N, int64_t K, int32_t kernel, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  rf_w8a16_proj q;
+  q.w_packed = w_packed;
+  q.scale = scale;
+  q.bias = bias;
+  q.y = y;
+  q.ldy = ldy;
+  q.N = N;
+  return rf_w4a16_linear_multi(x, ldx, &q, 1, group_size, M, K, kernel, workspace,
+                               workspace_bytes, stream);
 }
 
 size_t rf_w8a16_workspace_bytes_argmax(int64_t M, int64_t N, int64_t K) {

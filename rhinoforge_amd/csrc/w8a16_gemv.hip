@@ -74,7 +74,7 @@ struct GemvKernelArgs {
   // Group-wise int4: log2(group_size / 32); scale row of tile position k is
   // k / group_size.
   int gshift;
-  // Nonzero: groups per XCD run (xcd_group), the launch's groups / 8.
+  // Nonzero: workgroups per XCD run (xcd_map), the launch's groups * splits / 8.
   int xcd_run;
 };
 
@@ -268,27 +268,40 @@ __device__ __forceinline__ bool split_k_reduce(const GemvKernelArgs& a, int grou
 }
 
 // Fused argmax: this workgroup's per-row best keys (row_key, LDS) go to its
-// own slots with plain stores -- no atomics on shared addresses, which with
-// thousands of workgroups on one row would serialise -- and the next launch
-// on the stream (argmax_finish_kernel) reduces the slots.
+// group's own slots with plain stores -- no atomics on shared addresses,
+// which with thousands of workgroups on one row would serialise -- and the
+// next launch on the stream (argmax_finish_kernel) reduces the slots.
 __device__ __forceinline__ void argmax_store(const GemvKernelArgs& a, const unsigned long long* row_key,
-                                             int tid, int nthreads) {
+                                             int group, int tid, int nthreads) {
   __syncthreads();  // row_key complete
   for (int m = tid; m < a.M; m += nthreads)
-    a.amax_slots[(int64_t)m * gridDim.x + blockIdx.x] = row_key[m];
+    a.amax_slots[(int64_t)m * gridDim.x + group] = row_key[m];
 }
 
-// Group (strip range) of workgroup bx out of G.  The hardware deals
-// workgroups to the 8 XCDs round-robin by dispatch id, x fastest, so with
-// group = bx adjacent strips run on different XCDs.  A 128-byte line of a
-// group-wise scale row holds the scales of four adjacent strips (32 bytes
-// each), and every XCD's L2 would fetch it: four times the scale traffic.
-// Here the groups an XCD runs form one contiguous range of `run` = G / 8
-// groups (the first 8 * run workgroups; any rest keep their id), a bijection
-// of [0, G) either way; run = 0 keeps every id.  Branch-free, so the load of
-// `run` joins the kernel's other argument loads.
-__device__ __forceinline__ int xcd_group(int bx, int run) {
-  return bx < 8 * run ? (bx & 7) * run + (bx >> 3) : bx;
+// (group, K split) of this workgroup.  The hardware deals workgroups to the
+// 8 XCDs round-robin by linear dispatch id L = blockIdx.y * G + blockIdx.x
+// (G = gridDim.x groups, x fastest), so with the plain mapping adjacent
+// strips run on different XCDs and every XCD runs every K split:
+//   * a 128-byte line of a group-wise scale row holds the scales of four
+//     adjacent strips (32 bytes each), and every XCD's L2 fetches it;
+//   * every XCD's L2 fetches all of x, though each workgroup reads only its
+//     split's K slice.
+// With run > 0 the first 8 * run ids are dealt so that XCD x runs the
+// contiguous range [x * run, (x + 1) * run) of split-major order
+// v = split * G + group (any rest keep v = L): an XCD's workgroups cover
+// adjacent strips of one or two K splits.  A bijection of [0, G * S) either
+// way; run = G * S / 8 spreads every id.
+__device__ __forceinline__ void xcd_map(int run, int& group, int& split) {
+  const int G = gridDim.x;
+  const int L = blockIdx.y * G + blockIdx.x;
+  const int v = L < 8 * run ? (L & 7) * run + (L >> 3) : L;
+  if (gridDim.y == 1) {
+    group = v;
+    split = 0;
+  } else {
+    split = v / G;
+    group = v - split * G;
+  }
 }
 
 // WF (WeightFormat): int8 tiles (64 input positions, two MFMAs per tile and
@@ -306,22 +319,18 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-  const int group = GS ? xcd_group(blockIdx.x, a.xcd_run) : (int)blockIdx.x;
-  const int split = blockIdx.y;
-  // Projection of this workgroup (uniform across it).  Group-wise int4
-  // launches carry one projection (launch_gemv refuses more), so their
-  // argument loads need not wait for the remapped group.
+  int group = blockIdx.x, split = blockIdx.y;
+  if (a.xcd_run) xcd_map(a.xcd_run, group, split);
+  // Projection of this workgroup (uniform across it).  Its fields are loaded
+  // once pi is known, a second scalar-memory trip.  Reading one field of each
+  // 64-byte argument line with the first loads (the loop below reads the
+  // group0 of projections 1..3) brings every line into the scalar cache, so
+  // that trip hits it.
   int pi = 0;
-  if (!GS) {
-    // The projection's fields are loaded once pi is known, a second
-    // scalar-memory trip.  Reading one field of each 64-byte argument line
-    // with the first loads (the loop below reads the group0 of projections
-    // 1..3) brings every line into the scalar cache, so that trip hits it.
-    __asm__ volatile("" ::"s"(a.M), "s"(a.proj[0].group0), "s"(a.kb_per_split));
+  __asm__ volatile("" ::"s"(a.M), "s"(a.proj[0].group0), "s"(a.kb_per_split));
 #pragma unroll
-    for (int i = 1; i < kMaxProj; ++i)
-      if (i < a.nproj && group >= a.proj[i].group0) pi = i;
-  }
+  for (int i = 1; i < kMaxProj; ++i)
+    if (i < a.nproj && group >= a.proj[i].group0) pi = i;
   const uint8_t* const P_w = a.proj[pi].w;
   const _Float16* const P_scale = a.proj[pi].scale;
   const _Float16* const P_bias = a.proj[pi].bias;
@@ -584,7 +593,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   if (a.splits > 1 && !split_k_reduce<NS, !GS>(a, group, strip0, P_nstrips, P_N, P_col0, P_scale,
                                           P_bias, P_y, P_ldy, amax, row_key, tid, kThreads))
     return;
-  if (amax) argmax_store(a, row_key, tid, kThreads);
+  if (amax) argmax_store(a, row_key, group, tid, kThreads);
 }
 
 // One workgroup per row: the largest key over the GEMV's slots[m][0..G),
@@ -693,7 +702,7 @@ GemvKernelArgs make_args(const LinearProblem& pr, const GemvPlan& p, void* works
   int64_t wbytes = 0;
   for (int i = 0; i < pr.nproj; ++i) wbytes += (int64_t)pr.proj[i].N * pr.K / 2;
   const bool xcd = pr.wf == kWfInt4Grp && pr.gshift <= 1 && wbytes >= ((int64_t)16 << 20);
-  ka.xcd_run = xcd ? p.groups / 8 : 0;
+  ka.xcd_run = xcd ? p.groups * p.splits / 8 : 0;
   return ka;
 }
 
@@ -836,7 +845,7 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
   if (pr.nproj < 1 || pr.nproj > kMaxProj) return hipErrorInvalidValue;
   GemvKernelArgs ka = make_args(pr, p, workspace);
   if (pr.wf != kWfInt8) {
-    if (am || (pr.wf == kWfInt4Grp && pr.nproj != 1)) return hipErrorInvalidValue;
+    if (am) return hipErrorInvalidValue;
     return pr.wf == kWfInt4 ? launch_gemv4_cfg<kWfInt4>(ka, p, stream)
                             : launch_gemv4_cfg<kWfInt4Grp>(ka, p, stream);
   }
@@ -898,11 +907,14 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
 //     group-wise alike: 12288 x 4096 at M 5..16 7.3..9.1 against
 //     8.8..9.7 us; 24576 x 4096 at M 16 13.7 against 16.4 us, at M 8 12.3
 //     against 14.1 us; 25600 x 5120 at M 16 19.1 against 20.8 us).
-GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev) {
+GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
+                        const DeviceInfo& dev) {
   const int keff = (int)(round_up(K, kTileK4) / 2);
-  GemvPlan p = plan_gemv_rules(M, &N, 1, keff, dev, false);
+  GemvPlan p = plan_gemv_rules(M, Ns, nproj, keff, dev, false);
   const int ktiles = (int)ceil_div(K, kTileK4);
-  const int nstrips = (int)ceil_div(N, 16);
+  // The rules see the launch's strips of all projections together.
+  int nstrips = 0;
+  for (int i = 0; i < nproj; ++i) nstrips += (int)ceil_div(Ns[i], 16);
   const int cu = dev.cus > 0 ? dev.cus : 256;
   auto strips_ge = [&](int n256) { return (int64_t)nstrips * 256 >= (int64_t)n256 * cu; };
   auto fits_xl = [&](int w) { return gemv_lds_bytes(1, 1, w, true, M, ktiles, kTileK4) <= 65536; };
@@ -950,7 +962,8 @@ GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev
   q.cfg = cfg;
   q.mt = kGemvCfgs[cfg].mt;
   q.ns = kGemvCfgs[cfg].ns;
-  q.groups = (int)ceil_div(nstrips, q.ns);
+  q.groups = 0;
+  for (int i = 0; i < nproj; ++i) q.groups += (int)ceil_div(ceil_div(Ns[i], 16), q.ns);
   if (q.groups > kMaxGroupsSplit) splits = 1;
   if (splits > ktiles) splits = ktiles;
   q.kb_per_split = (int)ceil_div(ktiles, splits);

@@ -82,9 +82,11 @@ GemmPlan gemm_plan_for_stride(const GemmPlan& p, int M, const int* Ns, int nproj
 // int4: packed-int4 weights (TILE16X128_I4) take the large-tile rules only.
 GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
                    bool int4 = false);
-// GEMV plan of a packed-int4 weight (one projection); grouped: group-wise
-// scales (their per-tile scale loads change which configuration wins).
-GemvPlan plan_gemv_int4(int M, int N, int K, bool grouped, const DeviceInfo& dev);
+// GEMV plan of packed-int4 weights (nproj projections sharing x); grouped:
+// group-wise scales (their per-tile scale loads change which configuration
+// wins).
+GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
+                        const DeviceInfo& dev);
 // Workspace bytes past the RF_W8A16_WS_COUNTER_BYTES counter region.
 size_t gemv_workspace_bytes(const GemvPlan& p, int M, const int* Ns, int nproj);
 size_t gemm_workspace_bytes(const GemmPlan& p);

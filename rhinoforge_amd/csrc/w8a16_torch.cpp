@@ -13,6 +13,8 @@
 // and (namespace `w4a16`, packed int4 weights, rf_w4a16_* in the C ABI):
 //   linear(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias=None,
 //          int kernel=0) -> Tensor
+//   linear_multi(Tensor input, Tensor[] weights, Tensor[] weight_scales,
+//                Tensor?[] biases, int kernel=0) -> Tensor[]
 //   pack_weight(Tensor q) -> Tensor
 //   unpack_weight(Tensor packed, int N, int K) -> Tensor
 //
@@ -617,6 +619,100 @@ at::Tensor w4_linear_meta(const at::Tensor& input, const at::Tensor& weight, con
   return at::empty_symint(out_shape(input, sh.N), input.options());
 }
 
+// Several packed-int4 projections sharing the input (q/k/v, gate/up) in one
+// launch, as w8a16::linear_multi for int8.  All weight_scales have the same
+// rank (per-channel [N_i] or group-wise [K/gs, N_i] with one group size).
+// Returns the checked shapes (N_i) and the shared group size.
+std::pair<std::vector<c10::SymInt>, c10::SymInt> w4_check_multi(
+    const at::Tensor& input, at::TensorList weights, at::TensorList scales,
+    const c10::List<c10::optional<at::Tensor>>& biases, const char* op) {
+  const int64_t count = (int64_t)weights.size();
+  TORCH_CHECK(count >= 1 && count <= RF_W8A16_MAX_PROJ, op, ": between 1 and ",
+              RF_W8A16_MAX_PROJ, " projections, got ", count);
+  TORCH_CHECK((int64_t)scales.size() == count, op, ": ", count, " weights but ", scales.size(),
+              " weight_scales");
+  TORCH_CHECK(biases.size() == 0 || (int64_t)biases.size() == count, op, ": ", count,
+              " weights but ", biases.size(), " biases");
+  std::vector<c10::SymInt> Ns;
+  c10::SymInt gs0 = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const c10::optional<at::Tensor> b = biases.size() ? biases.get(i) : c10::optional<at::Tensor>();
+    const W4Shape sh = w4_check_shapes(input, weights[i], scales[i], b, op);
+    if (i == 0) gs0 = sh.group_size;
+    TORCH_CHECK(sh.group_size == gs0, op, ": every projection needs the same scale form and "
+                "group size (projection 0: ", gs0, ", projection ", i, ": ", sh.group_size, ")");
+    Ns.push_back(sh.N);
+  }
+  return {Ns, gs0};
+}
+
+std::vector<at::Tensor> w4_linear_multi_hip(const at::Tensor& input, at::TensorList weights,
+                                            at::TensorList scales,
+                                            const c10::List<c10::optional<at::Tensor>>& biases,
+                                            int64_t kernel) {
+  RECORD_FUNCTION("w4a16::linear_multi", {});
+  const char* op = "w4a16::linear_multi";
+  const auto chk = w4_check_multi(input, weights, scales, biases, op);
+  const int64_t count = (int64_t)weights.size();
+  const int64_t K = input.size(-1), group_size = chk.second.expect_int();
+  const int64_t M = input.numel() / K;
+  std::vector<at::Tensor> outs(count), keep(count);
+  rf_w8a16_proj projs[RF_W8A16_MAX_PROJ];
+  int64_t Ns[RF_W8A16_MAX_PROJ];
+  std::vector<int64_t> shape = input.sizes().vec();
+  for (int64_t i = 0; i < count; ++i) {
+    const c10::optional<at::Tensor> b = biases.size() ? biases.get(i) : c10::optional<at::Tensor>();
+    check_devices(input, weights[i], scales[i], b, op);
+    const int64_t N = chk.first[i].expect_int();
+    shape.back() = N;
+    outs[i] = at::empty(shape, input.options());  // contiguous: rows N apart
+    // group-wise scale rows are copied with 16-byte DMAs
+    keep[i] = (group_size && reinterpret_cast<uintptr_t>(scales[i].data_ptr()) % 16)
+                  ? scales[i].clone() : scales[i];
+    projs[i].w_packed = weights[i].data_ptr();
+    projs[i].scale = keep[i].data_ptr();
+    projs[i].bias = (b.has_value() && b->defined()) ? b->data_ptr() : nullptr;
+    projs[i].y = outs[i].data_ptr();
+    projs[i].ldy = N;
+    projs[i].N = N;
+    Ns[i] = N;
+  }
+  if (M == 0) return outs;
+  const at::Tensor x2 = compact_rows(input.dim() == 2 ? input : input.reshape({M, K}));
+  c10::DeviceGuard dev_guard(x2.device());
+  void* stream = c10::hip::getCurrentHIPStream(x2.device().index()).stream();
+  const int st = with_workspace(
+      x2.device(), stream, op,
+      [&](void* ws, size_t ws_bytes) {
+        return rf_w4a16_linear_multi(x2.data_ptr(), x2.stride(0), projs, (int32_t)count,
+                                     (int32_t)group_size, M, K, (int32_t)kernel, ws, ws_bytes,
+                                     stream);
+      },
+      [&] { return rf_w4a16_workspace_bytes_multi(M, Ns, (int32_t)count, K); });
+  check_status(st, op);
+  return outs;
+}
+
+std::vector<at::Tensor> w4_linear_multi_meta(const at::Tensor& input, at::TensorList weights,
+                                             at::TensorList scales,
+                                             const c10::List<c10::optional<at::Tensor>>& biases,
+                                             int64_t kernel) {
+  const auto chk = w4_check_multi(input, weights, scales, biases, "w4a16::linear_multi");
+  std::vector<at::Tensor> outs;
+  for (const c10::SymInt& N : chk.first)
+    outs.push_back(at::empty_symint(out_shape(input, N), input.options()));
+  return outs;
+}
+
+std::vector<at::Tensor> w4_linear_multi_cpu(const at::Tensor& input, at::TensorList weights,
+                                            at::TensorList scales,
+                                            const c10::List<c10::optional<at::Tensor>>& biases,
+                                            int64_t) {
+  w4_check_multi(input, weights, scales, biases, "w4a16::linear_multi");
+  TORCH_CHECK(false, "w4a16::linear_multi: tensors are on the CPU; the W4A16 kernels run on a "
+              "HIP device (gfx950) only and there is no CPU implementation");
+}
+
 at::Tensor w4_pack_weight_meta(const at::Tensor& q) {
   TORCH_CHECK(q.scalar_type() == at::kChar && q.dim() == 2 && q.sym_size(0) >= 1 &&
                   q.sym_size(1) >= 1,
@@ -733,26 +829,31 @@ TORCH_LIBRARY_IMPL(w8a16, Autograd, m) {
 TORCH_LIBRARY(w4a16, m) {
   m.def("linear(Tensor input, Tensor weight, Tensor weight_scale, Tensor? bias=None, "
         "int kernel=0) -> Tensor");
+  m.def("linear_multi(Tensor input, Tensor[] weights, Tensor[] weight_scales, Tensor?[] biases, "
+        "int kernel=0) -> Tensor[]");
   m.def("pack_weight(Tensor q) -> Tensor");
   m.def("unpack_weight(Tensor packed, int N, int K) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(w4a16, CUDA, m) {
   m.impl("linear", TORCH_FN(w4_linear_hip));
+  m.impl("linear_multi", TORCH_FN(w4_linear_multi_hip));
   m.impl("pack_weight", TORCH_FN(w4_pack_weight));
   m.impl("unpack_weight", TORCH_FN(w4_unpack_weight));
 }
 TORCH_LIBRARY_IMPL(w4a16, Meta, m) {
   m.impl("linear", TORCH_FN(w4_linear_meta));
+  m.impl("linear_multi", TORCH_FN(w4_linear_multi_meta));
   m.impl("pack_weight", TORCH_FN(w4_pack_weight_meta));
   m.impl("unpack_weight", TORCH_FN(w4_unpack_weight_meta));
 }
 TORCH_LIBRARY_IMPL(w4a16, CPU, m) {
   m.impl("linear", TORCH_FN(w4_linear_cpu));
+  m.impl("linear_multi", TORCH_FN(w4_linear_multi_cpu));
   m.impl("pack_weight", TORCH_FN(w4_pack_weight));
   m.impl("unpack_weight", TORCH_FN(w4_unpack_weight));
 }
 TORCH_LIBRARY_IMPL(w4a16, Autograd, m) {
-  for (const char* op : {"linear", "pack_weight", "unpack_weight"})
+  for (const char* op : {"linear", "linear_multi", "pack_weight", "unpack_weight"})
     m.impl(op, torch::CppFunction::makeFallthrough());
 }

@@ -178,3 +178,15 @@ def linear_w4a16(input: torch.Tensor, weight: torch.Tensor, weight_scale: torch.
     N % 16 == 0 and K % 64 == 0.  HIP tensors only.
     """
     return torch.ops.w4a16.linear(input, weight, weight_scale, bias, kernel)
+
+
+def linear_multi_w4a16(input: torch.Tensor, weights, weight_scales, biases=None, *,
+                       kernel: int = KERNEL_AUTO) -> list:
+    """Several packed-int4 projections of one input (q/k/v, gate/up) in one
+    launch of either kernel, as :func:`linear_multi` does for int8.  Every
+    scale has the same form: per-channel [N_i], or group-wise [K/gs, N_i]
+    with one group size.  Returns [input . W_i^T (+ b_i)]."""
+    weights = list(weights)
+    if biases is None:
+        biases = [None] * len(weights)
+    return torch.ops.w4a16.linear_multi(input, weights, list(weight_scales), list(biases), kernel)

@@ -80,12 +80,10 @@ static void plans() {
               rf_w8a16_plan_info info;
               std::memset(&info, 0x77, sizeof(info));
               const int st = rf_w8a16_plan(M, set, count, K, kernel, fmt, cus, &info);
-              if (fmt != RF_W8A16_FORMAT_INT8 && count != 1) {
-                CHECK(st == RF_W8A16_EINVAL);
-                continue;
-              }
-              // int4 packing needs N % 16 == 0 and K % 64 == 0 (rf_w4a16_linear)
-              if (fmt != RF_W8A16_FORMAT_INT8 && (set[0] % 16 != 0 || K % 64 != 0)) {
+              // int4 packing needs N % 16 == 0 and K % 64 == 0 (rf_w4a16_linear[_multi])
+              bool n16 = true;
+              for (int32_t i = 0; i < count; ++i) n16 = n16 && set[i] % 16 == 0;
+              if (fmt != RF_W8A16_FORMAT_INT8 && (!n16 || K % 64 != 0)) {
                 CHECK(st == RF_W8A16_EINVAL);
                 continue;
               }

@@ -841,6 +841,7 @@ def test_opcheck_on_device_tensors():
         (torch.ops.w8a16.linear_argmax.default, (x, w, s, None, True)),
         (torch.ops.w8a16.pack_weight.default, (q,)),
         (torch.ops.w4a16.linear.default, (x, w4, s4)),
+        (torch.ops.w4a16.linear_multi.default, (x, [w4, w4], [s4, s4], [b, None])),
         (torch.ops.w4a16.pack_weight.default, (q4,)),
     ]
     for op, args in cases:

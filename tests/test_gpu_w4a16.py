@@ -326,3 +326,49 @@ def test_w4a16_workspace_grows_on_a_fresh_stream(gs):
     torch.cuda.synchronize()
     assert torch.equal(y, ref)
     check(ref.cpu().numpy(), x, q, s, label=f"w4 workspace growth gs={gs}", rows=np.r_[0:8, m - 8:m])
+
+
+# Several packed-int4 projections in one launch (w4a16.linear_multi): the
+# Qwen3-8B q/k/v and gate/up groups at decode and prefill sizes, per-channel
+# and group-wise, a GEMV launch with a K split (long K, few strips) and one
+# with a group-wise XCD strip range (>= 16 MiB), and biases on some
+# projections.  Each output is checked against the oracle; the projections
+# sharing x also run as single launches, which must agree within the bar.
+MULTI = [
+    (1, [4096, 1024, 1024], 4096, 0), (1, [4096, 1024, 1024], 4096, 32),
+    (16, [4096, 1024, 1024], 4096, 128), (4, [12288, 12288], 4096, 0),
+    (16, [12288, 12288], 4096, 32), (64, [2048, 512], 1024, 32),
+    (3, [1024, 512], 16384, 0), (300, [1024, 512, 512], 2048, 32),
+    (130, [2048, 1024], 1024, 0),
+]
+
+
+@pytest.mark.parametrize("m,ns,k,gs", MULTI)
+def test_w4a16_linear_multi(m, ns, k, gs):
+    fmt = 2 if gs else 1
+    plan = capi.plan(m, ns, k, fmt=fmt)
+    _say(f"w4a16 multi M={m} Ns={ns} K={k} gs={gs}: {plan['name']} splits {plan['splits']}")
+    x = o8.make_activation(o8.derive_seed(9, "x4m", m, k), m, k)
+    ws, packed, scales, biases = [], [], [], []
+    for i, n in enumerate(ns):
+        w = o8.make_weight(o8.derive_seed(9, "w4m", i, n, k), n, k)
+        q, s = o4.quantize_int4_group_wise(w, gs) if gs else o4.quantize_int4_per_channel(w)
+        b = (o8.make_activation(o8.derive_seed(9, "b4m", i, n), 1, n)[0] * 0.1
+             if i == 1 else None)
+        ws.append((q, s, b))
+        packed.append(rf.pack_weight_int4(_dev(q)))
+        scales.append(_dev(s))
+        biases.append(None if b is None else _dev(b))
+    xd = _dev(x)
+    ys = rf.linear_multi_w4a16(xd, packed, scales, biases)
+    torch.cuda.synchronize()
+    for i, ((q, s, b), y) in enumerate(zip(ws, ys)):
+        assert y.shape == (m, ns[i])
+        got = y.cpu().numpy()
+        check(got, x, q, s, b, label=f"multi proj {i} N={ns[i]}")
+        single = rf.linear_w4a16(xd, packed[i], scales[i], biases[i]).cpu().numpy()
+        check(single, x, q, s, b, label=f"single proj {i} N={ns[i]}")
+    # deterministic: the split-K counters were left zero, same plan, same sums
+    again = rf.linear_multi_w4a16(xd, packed, scales, biases)
+    for a, b in zip(ys, again):
+        assert torch.equal(a, b)

@@ -48,6 +48,17 @@ def _cases():
         "w4a16::linear per-channel": (w4.linear.default,
                                       (_meta((3, 128), torch.float16), _meta(rf.packed_shape_int4(48, 128), torch.uint8),
                                        _meta((48,), torch.float16))),
+        "w4a16::linear_multi group-wise": (
+            w4.linear_multi.default,
+            (_meta((3, 128), torch.float16),
+             [_meta(rf.packed_shape_int4(48, 128), torch.uint8),
+              _meta(rf.packed_shape_int4(32, 128), torch.uint8)],
+             [_meta((4, 48), torch.float16), _meta((4, 32), torch.float16)],
+             [_meta((48,), torch.float16), None])),
+        "w4a16::linear_multi per-channel": (
+            w4.linear_multi.default,
+            (_meta((3, 128), torch.float16), [_meta(rf.packed_shape_int4(48, 128), torch.uint8)],
+             [_meta((48,), torch.float16)], [None])),
         "w4a16::pack_weight": (w4.pack_weight.default, (q4,)),
         "w4a16::unpack_weight": (w4.unpack_weight.default, (w4.pack_weight(q4), 48, 128)),
     }
@@ -133,5 +144,20 @@ def test_a_row_major_weight_is_refused_by_every_op():
         q4 = torch.zeros(4096, 2048, dtype=torch.uint8, device=dev)
         with pytest.raises(RuntimeError, match="packed int4 tiles"):
             w4.linear(x, q4, s)
+        with pytest.raises(RuntimeError, match="packed int4 tiles"):
+            w4.linear_multi(x, [q4, q4], [s, s], [None, None])
     with pytest.raises(RuntimeError, match="packed must have shape"):
         rf.unpack_weight(torch.zeros(4096, 4096, dtype=torch.int8), 4096, 4096)
+
+
+def test_w4a16_linear_multi_refuses_mixed_scale_forms():
+    x = _meta((3, 128), torch.float16)
+    w48, w32 = (_meta(rf.packed_shape_int4(n, 128), torch.uint8) for n in (48, 32))
+    with pytest.raises(RuntimeError, match="same scale form"):
+        torch.ops.w4a16.linear_multi(x, [w48, w32], [_meta((4, 48), torch.float16),
+                                                     _meta((32,), torch.float16)], [])
+    with pytest.raises(RuntimeError, match="same scale form"):
+        torch.ops.w4a16.linear_multi(x, [w48, w32], [_meta((4, 48), torch.float16),
+                                                     _meta((1, 32), torch.float16)], [])
+    with pytest.raises(RuntimeError, match="between 1 and 4"):
+        torch.ops.w4a16.linear_multi(x, [w48] * 5, [_meta((48,), torch.float16)] * 5, [])

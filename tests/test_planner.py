@@ -92,7 +92,10 @@ def test_int4_plans_and_errors():
     assert p["name"] == "gemm 128x128 B-in-registers"  # group-wise at M >= 1024
     p = capi.plan(520, [8192], 1024, fmt=capi.FORMAT_INT4_GROUP, cus=CUS)
     assert p["name"] == "gemm 128x128 interleaved"
+    # several int4 projections plan as one launch over their strips together
+    p = capi.plan(1, [4096, 1024, 1024], 4096, fmt=capi.FORMAT_INT4, cus=CUS)
+    assert p["kernel"] == "gemv" and p["workgroups"] == 384 // (p["tile_n"] // 16)  # 384 strips
     with pytest.raises(capi.W8A16Error):
-        capi.plan(4, [64, 64], 128, fmt=capi.FORMAT_INT4, cus=CUS)  # one projection only
+        capi.plan(4, [64, 40], 128, fmt=capi.FORMAT_INT4, cus=CUS)  # N % 16 != 0
     with pytest.raises(capi.W8A16Error, match="cannot run"):
         capi.plan(65, [64], 128, kernel=capi.KERNEL_GEMV, cus=CUS)
