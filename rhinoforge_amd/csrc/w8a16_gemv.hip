@@ -74,7 +74,7 @@ struct GemvKernelArgs {
   // Group-wise int4: log2(group_size / 32); scale row of tile position k is
   // k / group_size.
   int gshift;
-  // Nonzero: workgroups per XCD run (xcd_map), the launch's groups * splits / 8.
+  // Nonzero: groups per XCD run (xcd_group), the launch's groups / 8.
   int xcd_run;
 };
 
@@ -278,30 +278,19 @@ __device__ __forceinline__ void argmax_store(const GemvKernelArgs& a, const unsi
     a.amax_slots[(int64_t)m * gridDim.x + group] = row_key[m];
 }
 
-// (group, K split) of this workgroup.  The hardware deals workgroups to the
-// 8 XCDs round-robin by linear dispatch id L = blockIdx.y * G + blockIdx.x
-// (G = gridDim.x groups, x fastest), so with the plain mapping adjacent
-// strips run on different XCDs and every XCD runs every K split:
-//   * a 128-byte line of a group-wise scale row holds the scales of four
-//     adjacent strips (32 bytes each), and every XCD's L2 fetches it;
-//   * every XCD's L2 fetches all of x, though each workgroup reads only its
-//     split's K slice.
-// With run > 0 the first 8 * run ids are dealt so that XCD x runs the
-// contiguous range [x * run, (x + 1) * run) of split-major order
-// v = split * G + group (any rest keep v = L): an XCD's workgroups cover
-// adjacent strips of one or two K splits.  A bijection of [0, G * S) either
-// way; run = G * S / 8 spreads every id.
-__device__ __forceinline__ void xcd_map(int run, int& group, int& split) {
-  const int G = gridDim.x;
-  const int L = blockIdx.y * G + blockIdx.x;
-  const int v = L < 8 * run ? (L & 7) * run + (L >> 3) : L;
-  if (gridDim.y == 1) {
-    group = v;
-    split = 0;
-  } else {
-    split = v / G;
-    group = v - split * G;
-  }
+// Group (strip range) of workgroup bx out of G = gridDim.x.  The hardware
+// deals workgroups to the 8 XCDs round-robin by dispatch id, x fastest, so
+// with group = bx adjacent strips run on different XCDs.  A 128-byte line of
+// a group-wise scale row holds the scales of four adjacent strips (32 bytes
+// each), and every XCD's L2 would fetch it: up to four times the scale
+// traffic.  Here the groups an XCD runs form one contiguous range of
+// `run` = G / 8 groups (the first 8 * run workgroups of each split; any rest
+// keep their id), a bijection of [0, G) either way; run = 0 keeps every id.
+// The K split stays blockIdx.y, so the splits of one group keep sharing an
+// XCD when G % 8 == 0 (a split-major order, one K slice of x per XCD, measured
+// slower on every int8 and int4 K-split launch tried).
+__device__ __forceinline__ int xcd_group(int bx, int run) {
+  return bx < 8 * run ? (bx & 7) * run + (bx >> 3) : bx;
 }
 
 // WF (WeightFormat): int8 tiles (64 input positions, two MFMAs per tile and
@@ -319,8 +308,9 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-  int group = blockIdx.x, split = blockIdx.y;
-  if (a.xcd_run) xcd_map(a.xcd_run, group, split);
+  // (only group-wise launches renumber: the others need not wait for xcd_run)
+  const int group = GS ? xcd_group(blockIdx.x, a.xcd_run) : (int)blockIdx.x;
+  const int split = blockIdx.y;
   // Projection of this workgroup (uniform across it).  Its fields are loaded
   // once pi is known, a second scalar-memory trip.  Reading one field of each
   // 64-byte argument line with the first loads (the loop below reads the
@@ -692,17 +682,15 @@ GemvKernelArgs make_args(const LinearProblem& pr, const GemvPlan& p, void* works
                                                     RF_W8A16_WS_COUNTER_BYTES)
                          : nullptr;
   ka.amax_slots = nullptr;
-  // Contiguous strip ranges per XCD only where a group-wise scale's line
-  // over-fetch is a large share of the traffic: 32- and 64-wide groups (a
-  // scale row per 16 or 32 weight bytes of a channel) on launches of at least
-  // 16 MB of weights.  Graph-timed on MI355X, group size 32: Qwen3-8B gate,
-  // up and down at M = 1 11..12% faster, at M = 16 2..3%; launches of 8 MB or
-  // less 1..3% slower, and int8 q / o at M = 1..4 7..9% slower, so every other
-  // launch keeps the hardware's order.
-  int64_t wbytes = 0;
-  for (int i = 0; i < pr.nproj; ++i) wbytes += (int64_t)pr.proj[i].N * pr.K / 2;
-  const bool xcd = pr.wf == kWfInt4Grp && pr.gshift <= 1 && wbytes >= ((int64_t)16 << 20);
-  ka.xcd_run = xcd ? p.groups * p.splits / 8 : 0;
+  // Contiguous strip ranges per XCD on every group-wise launch: without them
+  // each XCD's L2 fetches the scale lines of its strips' neighbours too
+  // (FETCH_SIZE at M = 1, gs = 32: 1.34x the algorithmic bytes on 4096 x 4096
+  // and on the fused 24576 x 4096 gate/up, 1.12x on the fused q/k/v, against
+  // 1.003..1.016x with the ranges).  Graph-timed on MI355X: launches of 16 MB
+  // or more 5..12% faster at M = 1 and 2..3% at M = 16, smaller ones within
+  // +-2%; int8 launches (no scale lines) keep the hardware's order, which
+  // measured 7..9% faster on q / o at M = 1..4.
+  ka.xcd_run = pr.wf == kWfInt4Grp ? p.groups / 8 : 0;
   return ka;
 }
 
