@@ -180,6 +180,24 @@ static void refusals() {
                         nullptr, 0, nullptr) == RF_W8A16_EINVAL);  // N % 16
   CHECK(rf_w8a16_linear_argmax(x, 64, w, RF_W8A16_LAYOUT_TILE16X64, scale, nullptr, y, 64,
                                nullptr, 1, 64, 64, nullptr, 0, nullptr) == RF_W8A16_EINVAL);
+  // the fused int4 launch: the same refusals per projection, before any device query
+  rf_w8a16_proj p4[2] = {p, p};
+  CHECK(rf_w4a16_linear_multi(x, 64, p4, 2, 48, 1, 64, RF_W8A16_KERNEL_AUTO, nullptr, 0,
+                              nullptr) == RF_W8A16_EINVAL);  // group size
+  p4[1].N = 40;
+  CHECK(rf_w4a16_linear_multi(x, 64, p4, 2, 0, 1, 64, RF_W8A16_KERNEL_AUTO, nullptr, 0,
+                              nullptr) == RF_W8A16_EINVAL);  // N % 16 on the second projection
+  p4[1] = p;
+  CHECK(rf_w4a16_linear_multi(x, 64, p4, 5, 0, 1, 64, RF_W8A16_KERNEL_AUTO, nullptr, 0,
+                              nullptr) == RF_W8A16_EINVAL);  // count
+  CHECK(rf_w4a16_linear_multi(x, 64, p4, 2, 0, 1, 96, RF_W8A16_KERNEL_AUTO, nullptr, 0,
+                              nullptr) == RF_W8A16_EINVAL);  // K % 64
+  p4[1].scale = reinterpret_cast<uint8_t*>(scale) + 2;
+  CHECK(rf_w4a16_linear_multi(x, 64, p4, 2, 32, 1, 64, RF_W8A16_KERNEL_AUTO, nullptr, 0,
+                              nullptr) == RF_W8A16_EALIGN);  // group-wise scale 16-byte aligned
+  const int64_t ns4[2] = {64, 32};
+  CHECK(rf_w4a16_workspace_bytes_multi(1, ns4, 2, 64) >= RF_W8A16_WS_COUNTER_BYTES);
+  CHECK(rf_w4a16_workspace_bytes_multi(1, ns4, 0, 64) == 0);
   int8_t q[64];
   std::memset(q, 0, sizeof(q));
   CHECK(rf_w8a16_pack_weight(q, 0, 64, 64, w, sizeof(w)) == RF_W8A16_EINVAL);
