@@ -19,6 +19,10 @@ activations and outputs).  HIP events on the launch stream bracket the timed
 steps (preceded and followed by a device synchronize).  The steps are
 launched eagerly through the torch op.
 
+Graph replay: the same fused step captured GRAPH_STEPS at a time in one HIP
+graph and replayed (`config.graph_replay`), as a serving loop would run it;
+under a kernel tracer its dispatches run back to back.
+
 Distribution: a second pass of DIST_REPS steps records an event after every
 step; `stats` gives the median, p10 and p90 of the per-step rates (decode and
 prefill).  Per-launch rows (configs 0, 2, 4 and each projection) replay HIP
@@ -81,6 +85,8 @@ CFG0_COPIES = 192           # 192 x 3.1 MB = 605 MB
 LM_HEAD = (151936, 5120)
 ARGMAX_ROWS = 1000
 DIST_REPS = 60
+GRAPH_STEPS = 16            # decode steps per HIP graph (a multiple of the 4-copy rotation)
+GRAPH_REPLAYS = 3
 
 
 def nbytes(m, n, k, bias=False):
@@ -242,6 +248,7 @@ def bench_decode(torch, rf, steps, warmup):
             step_fused(warmup + i)
     fused_launches = steps * len(DECODE_M) * len(DECODE_GROUPS)
     fused_bytes = sum(group_bytes(m, g) for m in DECODE_M for g in DECODE_GROUPS)
+
     dist = step_times(torch, step_fused, DIST_REPS, warmup + steps)
 
     # The fused step per batch size (its 4 launches, same rotation), so the
@@ -283,6 +290,22 @@ def bench_decode(torch, rf, steps, warmup):
         sel = [r for r in rows if r["M"] == m and r["proj"] in dict((p, 1) for p, _, _ in QWEN3_8B)]
         per_m_per_op[str(m)] = round(sum(nbytes(m, r["N"], r["K"]) for r in sel)
                                      / sum(r["us"] * 1e-6 for r in sel) / 1e9, 1)
+    # The same step replayed from one HIP graph of GRAPH_STEPS steps (last:
+    # eager launches after graph replays measured slower in the same process): the
+    # launches a serving loop would capture once and replay.  Under a kernel
+    # tracer these dispatches run back to back (eager ones are traced one at a
+    # time), so their trace bounds the step without per-dispatch isolation.
+    def run_graph():
+        for i in range(GRAPH_STEPS):
+            step_fused(i)
+    g = capture(torch, run_graph)
+    g.replay()
+    with Timer(torch) as tg:
+        for _ in range(GRAPH_REPLAYS):
+            g.replay()
+    del g
+    graph_steps = GRAPH_STEPS * GRAPH_REPLAYS
+
     del layers
     torch.cuda.empty_cache()
     return {
@@ -292,6 +315,9 @@ def bench_decode(torch, rf, steps, warmup):
         "avg_launch_us": tf.ms * 1e3 / fused_launches,
         "avg_bytes_per_launch": fused_bytes / (len(DECODE_M) * len(DECODE_GROUPS)),
         "dist": rate_stats(dist, fused_bytes, 1e9),
+        "graph": {"GBps": round(fused_bytes * graph_steps / (tg.ms * 1e-3) / 1e9, 1),
+                  "ms_per_step": round(tg.ms / graph_steps, 4),
+                  "steps_per_graph": GRAPH_STEPS, "replays": GRAPH_REPLAYS},
         "per_M_fused_GBps": per_m_fused,
         "per_op_GBps": step_bytes * steps / (t.ms * 1e-3) / 1e9,
         "per_op_ms_per_step": t.ms / steps,
@@ -873,6 +899,7 @@ def main():
             "per_op_GBps": round(dec["per_op_GBps"], 1),
             "per_op_ms_per_step": round(dec["per_op_ms_per_step"], 4),
             "per_op_note": "the same step as 21 single-projection launches",
+            "graph_replay": dec["graph"],
         },
         "stats": {"decode_GBps": dec["dist"],
                   "prefill_TFLOPs": pre["dist"] if pre else None,
