@@ -999,7 +999,19 @@ void set_tiles(GemmPlan& p, int M, const int* Ns, int nproj) {
 static bool plan_two_k_groups(int M, const int* Ns, int nproj, int K, int cus, int64_t t128,
                               GemmPlan& out) {
   const int kblocks = (int)ceil_div(K, 64);
-  if (t128 > 128 || (kblocks >= 128 && t128 >= 96)) return false;
+  // One round of 129..CUs 128x128 tiles at M 128..512 with K <= 5120: the
+  // unsplit tile with two K groups, in place of the unsplit 3-stage tile
+  // (256 tiles) or two K splits with B in registers (the candidates below
+  // leave only it, since a split or a smaller tile no longer fits one round).
+  // Measured on nine shapes (MI355X, four rotated weight copies, same run):
+  // Qwen3-VL-32B q at M 512 45.6 -> 44.3 us, Qwen3-8B fused q/k/v at M 512
+  // 34.7 -> 33.0, fused gate/up at M 128 42.1 -> 37.6, Qwen3-VL-32B gate at
+  // M 128 53.0 -> 46.5, 12288 x 4096 at M 192 / 256 33.8 -> 32.6 / 35.1 ->
+  // 32.8, 8192 x 4096 at M 384 / 512 34.5 -> 32.9 / 38.6 -> 37.6, 16384 x
+  // 5120 at M 256 50.7 -> 49.3 (-2..-12%).  Longer K (Qwen3-VL-32B o and
+  // down at M 512) stays with the K-split plans, which measured faster.
+  const bool one_round = M >= 128 && M <= 512 && kblocks <= 80 && t128 <= cus;
+  if ((t128 > 128 && !one_round) || (kblocks >= 128 && t128 >= 96)) return false;
   // Beyond M 512 only where the forms measured faster: K <= 5120, at most
   // two K splits and >= 0.75 workgroups per CU.
   const bool beyond = M > 512;

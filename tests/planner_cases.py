@@ -197,10 +197,18 @@ GEMM_POLICY = [
     (128, 2048, 4104, "gemm 64x64 two K groups", 64, 64, 4),
     (129, 1040, 3016, "gemm 64x64 two K groups", 64, 64, 2),    # ragged M/N, K tail, 2 splits
     (512, 2056, 2120, "gemm 64x128 two K groups", 64, 128, 1),  # ragged N, 34 K blocks, K tail
-    # ... but not at K >= 8192 with >= 96 tiles, beyond 128 tiles, or below 16 K blocks
+    # ... and at 129..256 tiles (one round) with K <= 5120: the 128x128 tile
+    # with two K groups, unsplit
+    (384, 5504, 4096, "gemm 128x128 two K groups", 128, 128, 1),  # 129 tiles
+    (512, 8192, 5120, "gemm 128x128 two K groups", 128, 128, 1),  # Qwen3-VL-32B q at M = 512
+    (128, 24576, 4096, "gemm 128x128 two K groups", 128, 128, 1),  # 192 tiles
+    (300, 10000, 4104, "gemm 128x128 two K groups", 128, 128, 1),  # ragged M/N, K tail
+    # ... but not at K >= 8192 with >= 96 tiles, beyond 128 tiles otherwise,
+    # or below 16 K blocks
     (256, 6144, 8192, "gemm 128x128 B-in-registers", 128, 128, 5),
     (136, 8192, 8200, "gemm 128x128 B-in-registers", 128, 128, 4),
-    (384, 5504, 4096, "gemm 128x128 B-in-registers", 128, 128, 2),  # 129 tiles
+    (512, 8256, 5120, "gemm 128x128 interleaved", 128, 128, 1),  # 260 tiles
+    (512, 8192, 5184, "gemm 128x128 3-stage", 128, 128, 1),  # 81 K blocks
     (130, 520, 264, "gemm 128x128 3-stage", 128, 128, 1),
     # M < 128, 130 tile columns at K >= 8192: 64x256, 3-way K split
     (100, 16520, 8192, "gemm 64x256 3-stage", 64, 256, 3),
