@@ -882,8 +882,8 @@ enum GemmCfgId {
   kV3M32N128,     // 4 wavefronts 1x4, 4 stages, 3 workgroups/CU: M <= 32, >= 0.75 tiles per CU
   kV3M32N256,     // 4 wavefronts 1x4, 3 stages, 2 workgroups/CU: M <= 32, >= 0.75 tiles per CU
   kV3M128N128KG,  // two K groups of 4 wavefronts, 3 stages, 1 workgroup/CU: int8 M 33..2048,
-  kV3M64N128KG,   //   launches of few tiles (see plan_gemm), 128x128 / 64x128 / 64x64 tiles
-  kV3M64N64KG,    //   (64x64: 4 stages)
+  kV3M64N128KG,   //   launches of few tiles or one round of tiles (plan_two_k_groups),
+  kV3M64N64KG,    //   128x128 / 64x128 / 64x64 tiles (64x64: 4 stages)
   kGemmCfgCount
 };
 
