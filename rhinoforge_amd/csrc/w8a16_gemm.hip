@@ -239,8 +239,8 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   constexpr int S_OFF = A_BYTES + (BR ? 0 : B_BYTES);
   constexpr int SUB = S_OFF + S_BYTES;  // one K block's LDS
   constexpr int STAGE = KG * SUB;       // one block per K group
-  static_assert(KG == 1 || (KG == 2 && !BR && !IL && WF == kWfInt8),
-                "two K groups: int8, B in LDS, plain schedule");
+  static_assert(KG == 1 || (KG == 2 && !IL && WF == kWfInt8),
+                "two K groups: int8, plain schedule");
   constexpr int A_LOADS = A_BYTES / (NT * 16);
   constexpr int B_LOADS = BR ? 0 : B_BYTES / (NT * 16);
   constexpr int LOADS = A_LOADS + B_LOADS;
@@ -250,7 +250,12 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
   static_assert(!BR || (STAGES == 2 && WAVES_M == 1 && !IL), "register B: 2 stages, 1 x N grid");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
+  // Two K groups: group 1's accumulators are handed to group 0 through LDS
+  // at the end, which for the 128x256 register-B tile needs more than the
+  // stages hold.
+  constexpr int HANDOFF = KG == 2 ? WAVES_M * WAVES_N * TM * TN * 64 * 16 : 0;
+  constexpr int SMEM_BYTES = STAGES * STAGE > HANDOFF ? STAGES * STAGE : HANDOFF;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -390,8 +395,8 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(bbase), (short)0, -1, 0x00020000);
   // Issued right after the A DMA; the memory clobber keeps the compiler from
   // sinking them behind the MFMAs of the current block.
-  auto load_b = [&](int i) {
-    const int kb = kb0 + i;
+  auto load_b = [&](int i) {  // stage i (two K groups: this group's block, the last past the end)
+    const int kb = kb0 + (KG == 2 ? min(KG * i + kg_u, nk - 1) : i);
     const uint32_t boffk = WF ? (uint32_t)(kb >> 1) * kTileBytes + (kb & 1) * (kTileBytes / 2)
                               : (uint32_t)kb * kTileBytes;
 #pragma unroll
@@ -433,7 +438,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
     for (int j = 0; j < TN; ++j) __asm__ volatile("" ::"v"(bq[0][j]), "v"(bq[1][j]));
   };
   auto compute_br = [&](int i, const half8 (&bq)[2][TN]) {
-    const uint8_t* st = smem + (i % STAGES) * STAGE;
+    const uint8_t* st = smem + (i % STAGES) * STAGE + (KG == 2 ? kg_u * SUB : 0);
 #pragma unroll
     for (int step = 0; step < 2; ++step) {
       half8 af[TM];
@@ -556,11 +561,14 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
 
   if constexpr (BR) {
     // Two stages: A(i+1) by DMA and B(i+1) into registers are in flight
-    // during compute(i); every wait is a full vmcnt(0).
+    // during compute(i); every wait is a full vmcnt(0).  With two K groups
+    // a stage holds one block per group (as below), and a block past the
+    // split's end is loaded again and not multiplied.
+    const int nsb = (nk + KG - 1) / KG;
     issue(0, true);
     load_b(0);
     int i = 0;
-    for (; i < nk - 2; ++i) {
+    for (; i < nsb - 2; ++i) {  // the blocks issued here are never the split's last
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       barrier_lds();
       half8 bq[2][TN];
@@ -569,17 +577,22 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
       load_b(i + 1);
       compute_br(i, bq);
     }
-    for (; i < nk; ++i) {
+    for (; i < nsb; ++i) {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      if (k_tail && kb0 + i == a.kblocks - 1) fix_tail(i);
+      if constexpr (KG == 1) {
+        if (k_tail && kb0 + i == a.kblocks - 1) fix_tail(i);
+      } else {
+        if (k_tail && kb0 + nk - 1 == a.kblocks - 1 && i == (nk - 1) / KG && kg_u == (nk - 1) % KG)
+          fix_tail(nk - 1);
+      }
       barrier_lds();
       half8 bq[2][TN];
       dequant_b(i, bq);
-      if (i + 1 < nk) {
+      if (i + 1 < nsb) {
         issue(i + 1, true);
         load_b(i + 1);
       }
-      compute_br(i, bq);
+      if (KG == 1 || KG * i + kg_u < nk) compute_br(i, bq);
     }
   } else {
   const int ns = (nk + KG - 1) / KG;  // stages: one block per K group each
@@ -635,7 +648,7 @@ void w8a16_gemm_v3_kernel(GemmKernelArgs a) {
   if constexpr (KG == 2) {
     // Every wavefront is past its last compute, so the stages are free: group
     // 1 leaves its accumulators there and group 0 adds them to its own.
-    static_assert(NW * TM * TN * 64 * 16 <= STAGES * STAGE, "hand-off fits the stages");
+    static_assert(NW * TM * TN * 64 * 16 <= SMEM_BYTES, "hand-off fits the LDS");
     barrier_lds();
     floatx4* red = reinterpret_cast<floatx4*>(smem);
     if (kg_u == 1) {
@@ -884,6 +897,8 @@ enum GemmCfgId {
   kV3M128N128KG,  // two K groups of 4 wavefronts, 3 stages, 1 workgroup/CU: int8 M 33..2048,
   kV3M64N128KG,   //   launches of few tiles or one round of tiles (plan_two_k_groups),
   kV3M64N64KG,    //   128x128 / 64x128 / 64x64 tiles (64x64: 4 stages)
+  kV3M128N256KG,  // two K groups of the 128x256 register-B tile, 1 workgroup/CU: int8 long K
+                  //   in about one round of tiles (plan_long_k_two_groups)
   kGemmCfgCount
 };
 
@@ -892,11 +907,14 @@ constexpr int kGemmTile[kGemmCfgCount][3] = {{128, 256, 2}, {128, 128, 3}, {128,
                                              {64, 256, 2},  {128, 128, 1}, {32, 64, 4},
                                              {64, 64, 4},   {128, 128, 3}, {32, 128, 3},
                                              {32, 256, 2},  {128, 128, 1}, {64, 128, 1},
-                                             {64, 64, 1}};
+                                             {64, 64, 1},   {128, 256, 1}};
 
 // Wavefronts per workgroup of a configuration.
 int gemm_cfg_waves(int cfg) {
-  return (cfg == kV3M128N128KG || cfg == kV3M64N128KG || cfg == kV3M64N64KG) ? 8 : 4;
+  return (cfg == kV3M128N128KG || cfg == kV3M64N128KG || cfg == kV3M64N64KG ||
+          cfg == kV3M128N256KG)
+             ? 8
+             : 4;
 }
 
 // Short description of a configuration as it runs for weight format wf and
@@ -918,6 +936,7 @@ const char* gemm_cfg_name(int cfg, int wf, int M) {
     case kV3M128N128KG: return "128x128 two K groups";
     case kV3M64N128KG: return "64x128 two K groups";
     case kV3M64N64KG: return "64x64 two K groups";
+    case kV3M128N256KG: return "128x256 two K groups, B-in-registers";
     default: return "?";
   }
 }
@@ -1051,6 +1070,36 @@ static bool plan_two_k_groups(int M, const int* Ns, int nproj, int K, int cus, i
   return found;
 }
 
+// Long K (>= 8192) at M 512..2048 in about one round of 128x256 tiles (int8):
+// the 128x256 tile with B in registers as two K groups (eight wavefronts, one
+// workgroup per CU), with the fewest K splits (1..3) that bring the launch to
+// 0.75..1 workgroups per CU while each split keeps >= 96 K blocks.  Measured
+// on nine shapes against the plans they replace (MI355X, four rotated weight
+// copies, same run): Qwen3-8B down (4096 x 12288) at M 1024 / 1536 / 2048
+// 97.4 -> 89.5 / 133.4 -> 129.9 / 157.2 -> 152.9 us, Qwen3-VL-32B down (5120 x
+// 25600) at M 512 130.1 -> 122.4 us, 2048 x 12288 at M 2048 91.2 -> 88.0 us,
+// 4096 x 8192 at M 2048 106.1 -> 104.5 us (-1.4..-8%).  Not taken where no
+// split count fits (VL down at M 1024, 160 tiles: 253 -> 274 us) or the
+// splits would be shorter (4096 x 8192 at M 1024, 4096 x 12288 at M 512: even).
+static bool plan_long_k_two_groups(int M, const int* Ns, int nproj, int K, int cus,
+                                   GemmPlan& out) {
+  const int kblocks = (int)ceil_div(K, 64);
+  if (M < 512 || kblocks < 128) return false;
+  GemmPlan p;
+  p.cfg = kV3M128N256KG;
+  set_tiles(p, M, Ns, nproj);
+  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+  for (int s = 1; s <= 3; ++s) {
+    if (tiles * s > cus || kblocks < 96 * s || (s > 1 && tiles > kMaxSplitTiles)) return false;
+    if (4 * tiles * s < 3LL * cus) continue;
+    p.kb_per_split = (int)ceil_div(kblocks, s);
+    p.splits = (int)ceil_div(kblocks, p.kb_per_split);
+    out = p;
+    return true;
+  }
+  return false;
+}
+
 GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev, bool int4) {
   const int cus = dev.cus > 0 ? dev.cus : 256;
   if (M <= 32 && !int4) {
@@ -1121,6 +1170,7 @@ GemmPlan plan_gemm(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev
   if (!int4 && M <= 2048) {  // M >= 65 here
     GemmPlan kgp;
     if (plan_two_k_groups(M, Ns, nproj, K, cus, t128, kgp)) return kgp;
+    if (plan_long_k_two_groups(M, Ns, nproj, K, cus, kgp)) return kgp;
   }
   GemmPlan p;
   if (M < 128) {
@@ -1313,6 +1363,7 @@ hipError_t launch_gemm(const LinearProblem& pr, const GemmPlan& plan, void* work
     case kV3M128N128KG: return launch_v3_t<128, 128, 1, 4, 3, 1, kWfInt8, false, false, 2>(ka, stream);
     case kV3M64N128KG: return launch_v3_t<64, 128, 1, 4, 3, 1, kWfInt8, false, false, 2>(ka, stream);
     case kV3M64N64KG: return launch_v3_t<64, 64, 1, 4, 4, 1, kWfInt8, false, false, 2>(ka, stream);
+    case kV3M128N256KG: return launch_v3_t<128, 256, 1, 4, 2, 1, kWfInt8, false, true, 2>(ka, stream);
     default: return hipErrorInvalidValue;
   }
 }

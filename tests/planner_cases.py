@@ -234,8 +234,19 @@ GEMM_POLICY = [
     (1024, 2048, 8192, "gemm 128x128 B-in-registers", 128, 128, 5),
     # 160 tiles, 3-way split (two per CU): 128x128 with B in registers; K tail
     (500, 5000, 8200, "gemm 128x128 B-in-registers", 128, 128, 3),
-    # 256 tiles (one per CU), K >= 12288: 2-way K split
-    (1024, 4096, 12288, "gemm 128x128 B-in-registers", 128, 128, 2),
+    # 256 tiles (one per CU), K >= 12288, beyond M 2048: 2-way K split
+    (4096, 1024, 12288, "gemm 128x128 B-in-registers", 128, 128, 2),
+    # M 512..2048, K >= 8192: about one round of 128x256 tiles as two K groups
+    # with B in registers, the fewest splits (<= 3, >= 96 K blocks each) that
+    # reach 0.75 workgroups per CU
+    (2048, 4096, 12288, "gemm 128x256 two K groups, B-in-registers", 128, 256, 1),  # cfg3 down
+    (1024, 4096, 12288, "gemm 128x256 two K groups, B-in-registers", 128, 256, 2),
+    (512, 5120, 25600, "gemm 128x256 two K groups, B-in-registers", 128, 256, 3),  # VL down
+    (1500, 4000, 12296, "gemm 128x256 two K groups, B-in-registers", 128, 256, 1),  # ragged, K tail
+    (600, 5000, 24584, "gemm 128x256 two K groups, B-in-registers", 128, 256, 2),  # ragged, K tail
+    # ... but not where no split count fits one round, or below 96 K blocks per split
+    (1024, 5120, 25600, "gemm 128x128 B-in-registers", 128, 128, 2),  # 160 tiles
+    (520, 4096, 12288, "gemm 128x128 3-stage", 128, 128, 3),  # 3 splits of 64 K blocks
     # M <= 32: 32x64 tiles, 4-way K split (16 K blocks each)
     (20, 4096, 4096, "gemm 32x64 3-stage", 32, 64, 4),
     # M <= 32, K >= 192 blocks: 8-way split

@@ -77,12 +77,13 @@ def test_auto_kernel_choice_on_baseline_launches(args, kernel):
 
 def test_cfg3_prefill_plans():
     """The two timed prefill launches: 1536 tiles of 128x256 (three rounds of
-    the chip at two per CU) for fused gate/up; down: 512 tiles of 128x128 run
-    by the interleaved schedule (two per CU)."""
+    the chip at two per CU) for fused gate/up; down: 256 tiles of 128x256, one
+    eight-wavefront workgroup per CU (two K groups, B in registers)."""
     gu = capi.plan(2048, [12288, 12288], 4096, cus=CUS)
     assert (gu["name"], gu["workgroups"], gu["splits"]) == ("gemm 128x256 B-in-registers", 1536, 1)
     down = capi.plan(2048, [4096], 12288, cus=CUS)
-    assert (down["name"], down["workgroups"], down["splits"]) == ("gemm 128x128 interleaved", 512, 1)
+    assert (down["name"], down["workgroups"], down["splits"], down["waves"]) == \
+        ("gemm 128x256 two K groups, B-in-registers", 256, 1, 8)
 
 
 def test_int4_plans_and_errors():
