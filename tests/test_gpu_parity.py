@@ -1020,6 +1020,32 @@ def test_linear_multi_two_k_groups():
         assert_parity(y.cpu().numpy(), x, c[1], c[2], c[3], label=f"two K groups proj {i}")
 
 
+def test_linear_multi_long_k_two_k_groups():
+    """Two ragged projections at M = 1000 with K = 12296 (a K tail) in one
+    launch of the 128x256 register-B tile with two K groups and two K splits:
+    sampled rows (first and last included) of both outputs against the
+    oracle, and bit-identical to a second call."""
+    m, k = 1000, 12296
+    ns = [2056, 1000]
+    plan = capi.plan(m, ns, k, cus=256)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert (plan["name"], plan["splits"]) == ("gemm 128x256 two K groups, B-in-registers", 2), plan
+    _say(f"linear_multi long-K two K groups M={m} N={ns} K={k}")
+    cases = [make_case(m, n, k, seed=60 + i, bias=(i == 0)) for i, n in enumerate(ns)]
+    x = cases[0][0]
+    xd = _to_dev(x)
+    packed = [rf.pack_weight(_to_dev(c[1])) for c in cases]
+    scales = [_to_dev(c[2]) for c in cases]
+    biases = [None if c[3] is None else _to_dev(c[3]) for c in cases]
+    ys = rf.linear_multi(xd, packed, scales, biases)
+    again = rf.linear_multi(xd, packed, scales, biases)
+    torch.cuda.synchronize()
+    rows = np.concatenate([[0, m - 1], np.random.default_rng(m).choice(np.arange(1, m - 1), 62, replace=False)])
+    for i, (c, y, y2) in enumerate(zip(cases, ys, again)):
+        assert torch.equal(y, y2), i
+        assert_parity(y.cpu().numpy(), x, c[1], c[2], c[3], rows=rows, label=f"long-K two K groups proj {i}")
+
+
 def test_workspace_grows_on_a_fresh_stream():
     """The torch ops call the C ABI with the stream's cached workspace first
     (16 MB on a new stream) and grow it only when the call is refused with
