@@ -492,43 +492,85 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
       dma16(src, lds0 + j * 1024);
     }
   }
-  // The first two stages of weight tiles go out before anything waits.
-  if (stages > 0) load_stage(0, wA, xA, sA);
-  if (stages > 1) load_stage(1, wB, xB, sB);
-
   // ---- stage x[0:M, split's K range] in LDS (zero past K) ----------------
-  if (XL && KT) {
-    // Columns past K need zeros: staged through registers (after the first
-    // weight tiles went out, so the two round trips overlap).
-    const int row_chunks = ntiles * (TK / 8);
-    const int total = a.M * row_chunks;
-    for (int c = tid; c < total; c += kThreads) {
-      const int m = c / row_chunks, cc = c - m * row_chunks;
-      const int k = kb0 * TK + cc * 8;
-      const uint4 v = load_u4(a.x + (int64_t)m * a.ldx + min(k, a.K - 8));
-      *reinterpret_cast<uint4*>(smem + m * pitch + cc * 16) = k < a.K ? v : make_uint4(0, 0, 0, 0);
+  // Called once the first `issued` (0..2) weight stages are out.
+  auto stage_x = [&](int issued) {
+    if (XL && KT) {
+      // Columns past K need zeros: staged through registers (after the first
+      // weight tiles went out, so the two round trips overlap).
+      const int row_chunks = ntiles * (TK / 8);
+      const int total = a.M * row_chunks;
+      for (int c = tid; c < total; c += kThreads) {
+        const int m = c / row_chunks, cc = c - m * row_chunks;
+        const int k = kb0 * TK + cc * 8;
+        const uint4 v = load_u4(a.x + (int64_t)m * a.ldx + min(k, a.K - 8));
+        *reinterpret_cast<uint4*>(smem + m * pitch + cc * 16) = k < a.K ? v : make_uint4(0, 0, 0, 0);
+      }
+      __syncthreads();
+    } else if (XL) {
+      // The DMAs were issued before the weight loads (xdma above): wait for
+      // this wave's share (every load issued after them may stay in flight),
+      // then for everyone's.
+      // (loads per stage: U*NS weight tiles, and as many group scales)
+      constexpr int LPS = U * NS * (GS ? 2 : 1);
+      if (issued > 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPS) : "memory");
+      else if (issued > 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LPS) : "memory");
+      else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      barrier_lds();
     }
-    __syncthreads();
-  } else if (XL) {
-    // The DMAs were issued before the weight loads (xdma above): wait for
-    // this wave's share (every load issued after them may stay in flight),
-    // then for everyone's.
-    // (loads per stage: U*NS weight tiles, and as many group scales)
-    constexpr int LPS = U * NS * (GS ? 2 : 1);
-    if (stages > 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPS) : "memory");
-    else if (stages > 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(LPS) : "memory");
-    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    barrier_lds();
-  }
+  };
 
   // Two-stage pipeline, unrolled by two so the buffers never move: a
   // stage's buffer is refilled (two stages ahead) as soon as it is consumed.
-  for (int st = 0; st < stages; st += 2) {
+  // The compiler waits for a stage's loads by counting the loads issued
+  // after them, and where paths that issued different numbers of loads
+  // meet it must assume the fewest, i.e. wait for the next stage's loads
+  // too.  So with one m-tile (M <= 16) a wavefront with two or more stages
+  // takes a path on which every load is unconditional up to a tail of two
+  // or three stages: the prologue's two stages and both refills of the
+  // steady-state loop (which runs zero times for two or three stages); a
+  // stage is then computed as soon as its own loads are in, with the next
+  // one still in flight.  The instances with two or four m-tiles keep the
+  // plain loop: on that path the compiler holds more values live at once,
+  // and their register budget (up to four m-tiles of activations per
+  // stage) has no room for them.
+  if (MT == 1 && stages >= 2) {
+    load_stage(0, wA, xA, sA);
+    load_stage(1, wB, xB, sB);
+    stage_x(2);
+    int st = 0;
+    // (the scheduling barriers keep each refill ahead of the next stage's
+    // MFMAs, which the scheduler would otherwise interleave with it)
+    for (; st + 3 < stages; st += 2) {
+      compute_stage(st, wA, xA, sA);
+      load_stage(st + 2, wA, xA, sA);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_stage(st + 1, wB, xB, sB);
+      load_stage(st + 3, wB, xB, sB);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // two or three stages left, the last possibly partial
     compute_stage(st, wA, xA, sA);
-    if (st + 2 < stages) load_stage(st + 2, wA, xA, sA);
-    if (st + 1 >= stages) break;
-    compute_stage(st + 1, wB, xB, sB);
-    if (st + 3 < stages) load_stage(st + 3, wB, xB, sB);
+    if (st + 2 < stages) {
+      load_stage(st + 2, wA, xA, sA);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_stage(st + 1, wB, xB, sB);
+      compute_stage(st + 2, wA, xA, sA);
+    } else {
+      compute_stage(st + 1, wB, xB, sB);
+    }
+  } else {
+    // The first two stages of weight tiles go out before anything waits.
+    if (stages > 0) load_stage(0, wA, xA, sA);
+    if (stages > 1) load_stage(1, wB, xB, sB);
+    stage_x(stages);
+    for (int st = 0; st < stages; st += 2) {
+      compute_stage(st, wA, xA, sA);
+      if (st + 2 < stages) load_stage(st + 2, wA, xA, sA);
+      if (st + 1 >= stages) break;
+      compute_stage(st + 1, wB, xB, sB);
+      if (st + 3 < stages) load_stage(st + 3, wB, xB, sB);
+    }
   }
 
   floatx4 acc[MT][NS];
