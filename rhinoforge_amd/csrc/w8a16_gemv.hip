@@ -800,10 +800,9 @@ hipError_t launch_gemv_cfg(const GemvKernelArgs& ka, const GemvPlan& p, hipStrea
     case kG4x2W4U1: return launch_t<4, 2, 4, 1, false, true>(ka, p, stream);
     case kG1x3W8U2: return launch_t<1, 3, 8, 2, false, true>(ka, p, stream);
     case kG1x5W8U1: return launch_t<1, 5, 8, 1, false, true>(ka, p, stream);
-    case kG1x6W8U1: return launch_t<1, 6, 8, 1, false, true>(ka, p, stream);
     case kG1x7W8U1: return launch_t<1, 7, 8, 1, false, true>(ka, p, stream);
     case kG2x2W16U1: return launch_t<2, 2, 16, 1, false, true>(ka, p, stream);
-    default: return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;  // (kG1x6W8U1: planned for int4 only)
   }
 }
 
@@ -894,7 +893,7 @@ hipError_t launch_gemv(const LinearProblem& pr, const GemvPlan& p, void* workspa
 size_t argmax_slot_bytes(const GemvPlan& p, int M) { return (size_t)M * (size_t)p.groups * 8; }
 
 GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
-                         bool one_round);
+                         bool int8_rules);
 
 // Int4 launches: the int8 rules over K counted in 128-wide tiles (one 1 KB
 // tile per 128 positions), with these changes, measured on MI355X (cfg1 and
@@ -1011,12 +1010,14 @@ GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
 //     strips share it when there are enough strips to fill the chip;
 //   * M 17..64: two / four 16-row m-tiles per wavefront;
 //   * K splits only where the strips alone cannot fill 256 CUs.
-// one_round: the int8 rules at M 5..16 that give a workgroup three to seven
-// strips (kG1x3W8U2 .. kG1x7W8U1, sized to about one or two workgroups per
-// CU) and the 16-wavefront rule at M 17..32 (kG2x2W16U1); the int4 planner
-// starts from the rules without them.
+// int8_rules: the rules measured on int8 launches alone -- at M 5..16 the
+// ones that give a workgroup three to seven strips (kG1x3W8U2 .. kG1x7W8U1,
+// sized to about one or two workgroups per CU), eight wavefronts on 257..511
+// strips at long K and the 2-way K split at K >= 8192, and the 16-wavefront
+// rule at M 17..32 (kG2x2W16U1); the int4 planner starts from the rules
+// without them.
 GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInfo& dev,
-                         bool one_round) {
+                         bool int8_rules) {
   // Rules see the launch's strips of all projections together.
   int nstrips = 0;
   for (int i = 0; i < nproj; ++i) nstrips += (int)ceil_div(Ns[i], 16);
@@ -1065,19 +1066,22 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
       // it costs less): three strips per workgroup (Qwen3-14B lm_head
       // 151936 x 5120 at M 8: 117.9 instead of 119.6 us; 32768 x 4096:
       // 23.3 instead of 25.1 us).
-      cfg = (one_round && M <= 8) ? kG1x3W8U2 : kG1x4W4U2;
-    } else if (one_round && strips_ge(1025) && spc <= 7) {
+      cfg = (int8_rules && M <= 8) ? kG1x3W8U2 : kG1x4W4U2;
+    } else if (int8_rules && strips_ge(1025) && spc <= 7) {
       // 5..7 strips per CU: that many strips per 8-wave workgroup, one
       // workgroup per CU, so each activation fragment serves 5..7 weight
-      // tiles; at 6 per CU and M <= 12 three strips, two workgroups per CU
-      // (MI355X, four rotated weight copies: Qwen3-8B fused gate/up
-      // 24576 x 4096 at M 16: 18.8 instead of 21.6 us, at M 5..12 17.7..18.0
-      // instead of 18.9..20.6 us; 20480 x 4096 at M 16: 16.1 instead of
-      // 20.2 us; 28672 x 4096: 21.7 instead of 25.9 us).
-      cfg = spc == 5 ? kG1x5W8U1 : spc == 7 ? kG1x7W8U1 : M <= 12 ? kG1x3W8U2 : kG1x6W8U1;
+      // tiles; at 6 per CU three strips, two workgroups per CU (MI355X, four
+      // rotated weight copies: Qwen3-8B fused gate/up 24576 x 4096 at M 16:
+      // 18.8 instead of 21.6 us, at M 5..12 17.7..18.0 instead of 18.9..20.6
+      // us; 20480 x 4096 at M 16: 16.1 instead of 20.2 us; 28672 x 4096:
+      // 21.7 instead of 25.9 us).  Since each wavefront waits only for its
+      // own stage (the one-m-tile pipeline), three strips also beat six at
+      // M 13..16: 24576 x 4096 at M 16 18.1 against 18.6 us (graph-timed,
+      // 600 MB of rotated weights, three interleaved rounds).
+      cfg = spc == 5 ? kG1x5W8U1 : spc == 7 ? kG1x7W8U1 : kG1x3W8U2;
     } else if (strips_ge(1024)) {
       cfg = kG1x2W8U2;
-    } else if (one_round && strips_ge(513) && spc == 3) {
+    } else if (int8_rules && strips_ge(513) && spc == 3) {
       // 3 strips per CU: three strips per 8-wave workgroup, one workgroup
       // per CU (12288 x 4096 at M 5 / 8 / 16: 10.4 / 10.9 / 11.2 instead of
       // 12.6 / 12.8 / 13.1 us with four strips per workgroup).
@@ -1087,10 +1091,21 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
     } else if (strips_ge(512)) {
       cfg = kG1x2W8U2;  // 512 strips: four per workgroup leaves half the CUs idle
     } else if (strips_ge(257)) {
-      cfg = kG1x2W16U2;
+      // From K 5120 eight wavefronts of twice the tiles each stream longer
+      // than sixteen (5120 x 5120 at M 5 / 8 / 12 / 16: 7.4 / 8.1 / 9.0 /
+      // 10.0 against 8.0 / 8.7 / 9.8 / 10.8 us; at K 4096 the two tie).
+      cfg = (int8_rules && kblocks >= 80) ? kG1x2W8U2 : kG1x2W16U2;
     } else if (kblocks >= 128) {
-      cfg = kG1x4W8U2;
-      splits = 4;
+      if (int8_rules && strips_ge(129)) {
+        // 129..256 strips: two strips per workgroup and a 2-way K split
+        // (Qwen3-8B down 4096 x 12288 at M 8 / 12 / 16: 11.4 / 12.1 / 13.0
+        // against 12.2 / 12.9 / 13.1 us with four strips and four splits).
+        cfg = kG1x2W8U2;
+        splits = 2;
+      } else {
+        cfg = kG1x4W8U2;
+        splits = 4;
+      }
     } else if (!strips_ge(65)) {
       cfg = kG1x2W16U2;
       splits = 4;
@@ -1103,7 +1118,7 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
     } else if (kblocks >= 128) {
       cfg = kG2x4W4U2;
       splits = 4;
-    } else if (one_round && !strips_ge(129) && kblocks >= 64) {
+    } else if (int8_rules && !strips_ge(129) && kblocks >= 64) {
       // <= 128 strips, K 4096..8191 (int8): two strips per 16-wavefront
       // workgroup and a 4-way K split (MI355X, 600 MB of rotated weights:
       // Qwen3-8B k and v together, 2048 x 4096, at M 24 / 32 7.6 / 8.0

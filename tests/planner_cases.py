@@ -39,14 +39,14 @@ GEMV_POLICY = [
     # M 5..8, >=2048 strips: three strips per 8-wave workgroup
     (8, 32768, 128, "gemv 1x3 strips, 8 waves", 16, 48, 1),
     (5, 40016, 136, "gemv 1x3 strips, 8 waves", 16, 48, 1),    # ragged N (2501 strips), K tail
-    # M 5..16, 1025..1792 strips (5..7 per CU): one workgroup per CU
+    # M 5..16, 1025..1792 strips (5 or 7 per CU): one workgroup per CU
     (16, 20480, 256, "gemv 1x5 strips, 8 waves", 16, 80, 1),
-    (16, 24576, 512, "gemv 1x6 strips, 8 waves", 16, 96, 1),
-    (13, 24000, 200, "gemv 1x6 strips, 8 waves", 16, 96, 1),   # ragged N (1500 strips), K tail
     (16, 28672, 128, "gemv 1x7 strips, 8 waves", 16, 112, 1),
     (9, 26000, 320, "gemv 1x7 strips, 8 waves", 16, 112, 1),    # 1625 strips
-    # 6 per CU at M <= 12: three strips, two workgroups per CU
+    # 6 per CU: three strips, two workgroups per CU
     (12, 24576, 512, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    (16, 24576, 512, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    (13, 24000, 200, "gemv 1x3 strips, 8 waves", 16, 48, 1),   # ragged N (1500 strips), K tail
     # M 3..4 at 1536 strips keeps two strips per workgroup
     (4, 24576, 256, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     # M 5..16, >=1024 strips: two strips per 8-wave workgroup
@@ -58,7 +58,12 @@ GEMV_POLICY = [
     (16, 12288, 4096, "gemv 1x3 strips, 8 waves", 16, 48, 1),
     # M 5..16, 257..511 strips: two strips per 16-wave workgroup
     (10, 5000, 512, "gemv 1x2 strips, 16 waves", 16, 32, 1),
-    # M 5..16, long K: 4-way K split
+    # the same from K 5120: two strips per 8-wave workgroup
+    (16, 5120, 5120, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 5..16, long K, 129..256 strips: two strips per workgroup, 2-way K split
+    (16, 4096, 12288, "gemv 1x2 strips, 8 waves", 16, 32, 2),
+    (5, 2056, 8200, "gemv 1x2 strips, 8 waves", 16, 32, 2),     # ragged N and K
+    # M 5..16, long K, fewer strips: 4-way K split
     (16, 1024, 8192, "gemv 1x4 strips, 8 waves", 16, 64, 4),
     # M 5..16, <=64 strips: 4-way K split
     (9, 1000, 1024, "gemv 1x2 strips, 16 waves", 16, 32, 4),
@@ -277,7 +282,7 @@ GEMM_POLICY = [
 STRIP_GROUP_LAUNCHES = [
     (16, [4000, 4000, 1032], 1032, "gemv 1x3 strips, 8 waves"),
     (16, [10000, 10480], 512, "gemv 1x5 strips, 8 waves"),
-    (13, [12000, 12008, 264], 256, "gemv 1x6 strips, 8 waves"),
+    (13, [12000, 12008, 264], 256, "gemv 1x3 strips, 8 waves"),
     (9, [12000, 12000], 456, "gemv 1x3 strips, 8 waves"),
     (16, [9000, 9000, 9000], 320, "gemv 1x7 strips, 8 waves"),
     (6, [20000, 20000, 40], 192, "gemv 1x3 strips, 8 waves"),
