@@ -397,10 +397,13 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   half8 xA[XL ? 1 : U][MT][XN], xB[XL ? 1 : U][MT][XN];
   _Float16 sA[GS ? U : 1][NS], sB[GS ? U : 1][NS];
 
+  // nvalid < U (a wave-uniform count, U at every pipelined call): only the
+  // stage's first nvalid tiles are loaded; see the one-stage path below.
   auto load_stage = [&](int st, uint4 (&wv)[U][NS], half8 (&xv)[XL ? 1 : U][MT][XN],
-                        _Float16 (&sv)[GS ? U : 1][NS]) {
+                        _Float16 (&sv)[GS ? U : 1][NS], int nvalid) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      if (u >= nvalid) break;  // wave-uniform
       const int kl = wave + W * (st * U + u);
       const int klc = min(kl, ntiles - 1);
 #pragma unroll
@@ -535,41 +538,57 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
   // and their register budget (up to four m-tiles of activations per
   // stage) has no room for them.
   if (MT == 1 && stages >= 2) {
-    load_stage(0, wA, xA, sA);
-    load_stage(1, wB, xB, sB);
+    load_stage(0, wA, xA, sA, U);
+    load_stage(1, wB, xB, sB, U);
+    // (the prologue's loads all go out before any MFMA: the scheduler would
+    // otherwise sink each tile's loads to just before its use)
+    __builtin_amdgcn_sched_barrier(0);
     stage_x(2);
     int st = 0;
     // (the scheduling barriers keep each refill ahead of the next stage's
     // MFMAs, which the scheduler would otherwise interleave with it)
     for (; st + 3 < stages; st += 2) {
       compute_stage(st, wA, xA, sA);
-      load_stage(st + 2, wA, xA, sA);
+      load_stage(st + 2, wA, xA, sA, U);
       __builtin_amdgcn_sched_barrier(0);
       compute_stage(st + 1, wB, xB, sB);
-      load_stage(st + 3, wB, xB, sB);
+      load_stage(st + 3, wB, xB, sB, U);
       __builtin_amdgcn_sched_barrier(0);
     }
     // two or three stages left, the last possibly partial
     compute_stage(st, wA, xA, sA);
     if (st + 2 < stages) {
-      load_stage(st + 2, wA, xA, sA);
+      load_stage(st + 2, wA, xA, sA, U);
       __builtin_amdgcn_sched_barrier(0);
       compute_stage(st + 1, wB, xB, sB);
       compute_stage(st + 2, wA, xA, sA);
     } else {
       compute_stage(st + 1, wB, xB, sB);
     }
+  } else if (stages <= 1) {
+    // At most one stage: its loads all go out before any MFMA (the
+    // scheduling barrier: the scheduler would otherwise sink each tile's
+    // loads to just before its use, one memory round trip per tile).  A
+    // partial stage loads only its tiles (nothing is pipelined behind it);
+    // the x copy's exact wait counts a full stage, so it then waits for
+    // every load.
+    const bool full = my >= U;
+    if (stages > 0) load_stage(0, wA, xA, sA, full ? U : my);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_x(full ? stages : 0);
+    if (stages > 0) compute_stage(0, wA, xA, sA);
   } else {
     // The first two stages of weight tiles go out before anything waits.
-    if (stages > 0) load_stage(0, wA, xA, sA);
-    if (stages > 1) load_stage(1, wB, xB, sB);
+    load_stage(0, wA, xA, sA, U);
+    load_stage(1, wB, xB, sB, U);
+    __builtin_amdgcn_sched_barrier(0);
     stage_x(stages);
     for (int st = 0; st < stages; st += 2) {
       compute_stage(st, wA, xA, sA);
-      if (st + 2 < stages) load_stage(st + 2, wA, xA, sA);
+      if (st + 2 < stages) load_stage(st + 2, wA, xA, sA, U);
       if (st + 1 >= stages) break;
       compute_stage(st + 1, wB, xB, sB);
-      if (st + 3 < stages) load_stage(st + 3, wB, xB, sB);
+      if (st + 3 < stages) load_stage(st + 3, wB, xB, sB, U);
     }
   }
 
