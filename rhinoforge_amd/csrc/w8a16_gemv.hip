@@ -496,7 +496,9 @@ __global__ __launch_bounds__(W * 64) void w8a16_gemv_kernel(GemvKernelArgs a) {
     }
   }
   // ---- stage x[0:M, split's K range] in LDS (zero past K) ----------------
-  // Called once the first `issued` (0..2) weight stages are out.
+  // Called once the first weight stages are out; `issued` (0..2) full
+  // stages of them may stay in flight past the x copy's wait (0: that wait
+  // covers every load issued so far).
   auto stage_x = [&](int issued) {
     if (XL && KT) {
       // Columns past K need zeros: staged through registers (after the first
