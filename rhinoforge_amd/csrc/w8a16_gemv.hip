@@ -1067,8 +1067,12 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
       cfg = kG1x2W16U2;
     } else if (kblocks >= 128 || (M == 1 && kblocks >= 80)) {
       // (at M = 1 from K = 5120: ten tiles per wavefront instead of five,
-      // Qwen3-VL-32B k/v 1024 x 5120 4.84 instead of 5.15 us)
-      cfg = (M == 1 && lds_fits(kG1x1W8U4XL, M, kblocks)) ? kG1x1W8U4XL : kG1x1W8U4;
+      // Qwen3-VL-32B k/v 1024 x 5120 4.84 instead of 5.15 us).  x is staged
+      // in LDS at M = 1, and for int8 at M = 2 from K 8192 too (Qwen3-8B down
+      // 4096 x 12288 at M = 2: 10.1..10.5 against 10.7..11.8 us, three
+      // rounds, graph-timed, 600 MB of rotated weights).
+      const bool xl = M == 1 || (int8_rules && M == 2 && kblocks >= 128);
+      cfg = (xl && lds_fits(kG1x1W8U4XL, M, kblocks)) ? kG1x1W8U4XL : kG1x1W8U4;
     } else if (kblocks <= 16) {
       // K <= 1024: four wavefronts of four tiles, one pipeline stage each,
       // and a 4-way cross-wavefront sum instead of 16 (Qwen3-0.6B q/k/v

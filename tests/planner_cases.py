@@ -21,6 +21,8 @@ GEMV_POLICY = [
     (1, 512, 8192, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
     # M<=4, long K: 8 wavefronts, x from global memory
     (3, 512, 8192, "gemv 1x1 strips, 8 waves", 16, 16, 1),
+    # the same at M=2 from K 8192: x in LDS (int8)
+    (2, 4096, 12288, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
     # M=1, default: x in LDS, 16 wavefronts
     (1, 512, 4096, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
     # same, x copy ends mid-way through a 1 KB DMA chunk
