@@ -30,6 +30,8 @@
 //
 // The per-channel scale is applied once in the epilogue: s[n] factors out
 // of the K sum, y[m,n] = s[n] * sum_k x[m,k] q[n,k] (+ b[n]).
+#include <algorithm>
+
 #include "w8a16_common.h"
 #include "w8a16_internal.h"
 #include "../../include/w8a16.h"
@@ -1022,6 +1024,126 @@ GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
 }
 
 
+// Int8 rules at M <= 16 measured over the decode projections of the
+// reference's model families -- Qwen3 0.6B / 1.7B / 4B / 8B / 14B / 32B and
+// Qwen3-VL-32B, Qwen2.5-VL 3B / 7B, the Pi0.5 Gemma decoder (2048 wide, MLP
+// 16384) and action expert (1024 wide, MLP 4096), each projection alone and
+// q/k/v and gate/up fused, at M 1..16 -- against every configuration and K
+// split (MI355X, graph-timed, 600 MB of rotated weights, three interleaved
+// rounds).  Sets cfg / splits and returns true where they replace the
+// general rules below; returns false elsewhere.
+//   * M <= 4 on 257..639 strips from K 1088: two strips per 8-wave
+//     workgroup, no K split (Qwen3-14B q 5120 x 5120 at M 1 / 2: 7.0 against
+//     7.7 / 7.9 us with x in LDS; Qwen3-14B down 5120 x 17408: 17.5 against
+//     19.6 us with an 8-way split; Qwen3-4B q/k/v 6144 x 2560: 5.25 against
+//     5.53 us with 16 wavefronts), except at M <= 2 for K 8192..16383, where
+//     x in LDS and two strips tie to within the spread between boxes
+//     (Qwen3-VL-32B o 5120 x 8192: -2.6..+4.5%);
+//   * M <= 4 below 257 strips from K 1088: x staged in LDS at M 1 and 2, at
+//     M 3 below 256 strips and at M 4 up to 128, with a 2-way K split where
+//     only that fits (Qwen3-0.6B down 1024 x 3072 at M 2: 3.68 against 4.32
+//     us; Qwen2.5-VL-7B down 3584 x 18944 at M 1: 12.9 against 16.7 us;
+//     Qwen2.5-VL-3B down 2048 x 11008 at M 3: 8.2 against 9.6 us); else 16
+//     wavefronts, or from K 16384 two strips per workgroup split to about
+//     one workgroup per CU (Qwen3-8B down at M 4: 10.7 against 11.1 us with
+//     8 wavefronts; Qwen2.5-VL-7B down at M 2..4: 14.3..14.6 against
+//     17.0..17.7 us);
+//   * M 5..16 on >= 2048 strips: from M 9 and K 3072 five strips per
+//     8-wave workgroup (Qwen3-14B gate/up 34816 x 5120 at M 16: 31.9
+//     against 37.7 us with four strips per 4-wave workgroup; Qwen2.5-VL-7B
+//     gate/up 37888 x 3584: 23.5 against 27.4 us; Qwen3-14B lm_head 151936
+//     x 5120 ties; at K 2048, Pi0.5 gate/up 32768 x 2048, four per 4-wave
+//     workgroup stay 7% faster), and at M 5..8 from K 1088 three or five strips,
+//     whichever keeps the rounds of 256 workgroups fuller (Qwen2.5-VL-7B
+//     gate/up at M 8: five, 22.6 against 26.7 us with three; the Qwen3-14B
+//     lm_head stays at three, 116.7 us at M 8);
+//   * M 5..16 from K 16384: five strips per workgroup and a 4-way K split on
+//     257..511 strips (Qwen3-14B down at M 16: 19.6 against 25.1 us with two
+//     strips and 8 splits), four strips on 129..256 (Qwen2.5-VL-7B down at
+//     M 16: 16.6 against 21.5 us), two on fewer;
+//   * M 5..16, K 8192..16383, up to 128 strips: two strips, 4-way K split
+//     (Qwen2.5-VL-3B down at M 16: 10.2 against 11.3 us with four strips);
+//     on 129..256 strips at M 5..6: one strip per 16-wave workgroup, no
+//     split (Qwen3-8B down at M 5: 10.8 against 11.7 us with two strips and
+//     two splits);
+//   * M 5..16 on <= 64 strips: one strip per 16-wave workgroup and no K
+//     split, or at M >= 8 from K 5120 one per 8-wave workgroup and a 4-way
+//     split (Pi0.5 expert o 1024 x 2048 at M 8: 3.8 against 5.9 us with
+//     two strips and four splits; Qwen3-14B k 1024 x 5120 at M 16: 6.6
+//     against 7.2 us).
+static bool plan_int8_rules(int M, int nstrips, int kblocks, int cu, int* cfg, int* splits) {
+  auto strips_ge = [&](int n256) { return (int64_t)nstrips * 256 >= (int64_t)n256 * cu; };
+  auto groups = [&](int ns) { return (nstrips + ns - 1) / ns; };
+  *splits = 1;
+  if (M > 16 || (M <= 4 && kblocks <= 16)) return false;
+  if (M <= 4) {
+    if (strips_ge(640) || (strips_ge(512) && kblocks >= 256)) return false;
+    if (strips_ge(257)) {
+      if (M <= 2 && kblocks >= 128 && kblocks < 256) return false;
+      *cfg = kG1x2W8U2;
+      return true;
+    }
+    // (M 1, K 4096..5119, <= 64 strips: sixteen wavefronts of one stage
+    // each stay 2% faster, Qwen3-8B k 1024 x 4096)
+    if (M == 1 && kblocks >= 64 && kblocks < 80 && !strips_ge(65)) return false;
+    const bool few = !strips_ge(129);
+    const bool xl_rows = M <= 2 || (M == 3 && !strips_ge(256)) || (M == 4 && few);
+    if (xl_rows && lds_fits(kG1x1W8U4XL, M, kblocks)) {
+      *cfg = kG1x1W8U4XL;
+    } else if (xl_rows && few && lds_fits(kG1x1W8U4XL, M, (kblocks + 1) / 2)) {
+      *cfg = kG1x1W8U4XL;
+      *splits = 2;
+    } else if (kblocks >= 256) {
+      *cfg = kG1x2W8U2;
+      *splits = std::max(1, std::min(8, (cu + groups(2) / 2) / groups(2)));
+    } else {
+      *cfg = kG1x1W16U2;
+    }
+    return true;
+  }
+  if (strips_ge(2048)) {
+    if (kblocks <= 16) return false;
+    if (M >= 9) {
+      if (kblocks < 48) return false;
+      *cfg = kG1x5W8U1;
+    } else {
+      // Busy share of the rounds of `cu` workgroups the launch needs.
+      auto fill = [&](int ns) {
+        const int g = groups(ns);
+        return (double)g / (double)(((g + cu - 1) / cu) * cu);
+      };
+      *cfg = fill(5) > fill(3) ? kG1x5W8U1 : kG1x3W8U2;
+    }
+    return true;
+  }
+  if (strips_ge(512)) return false;
+  if (kblocks >= 256) {
+    *cfg = strips_ge(257) ? kG1x5W8U1 : strips_ge(129) ? kG1x4W8U2 : kG1x2W8U2;
+    *splits = 4;
+    return true;
+  }
+  if (strips_ge(257)) return false;
+  if (kblocks >= 128) {
+    if (!strips_ge(129)) {
+      *cfg = kG1x2W8U2;
+      *splits = 4;
+      return true;
+    }
+    if (M <= 6) {
+      *cfg = kG1x1W16U2;
+      return true;
+    }
+    return false;
+  }
+  if (!strips_ge(65)) {
+    const bool split = M >= 8 && kblocks >= 80;
+    *cfg = split ? kG1x1W8U4 : kG1x1W16U2;
+    *splits = split ? 4 : 1;
+    return true;
+  }
+  return false;
+}
+
 // Kernel choice per shape: the analogue of the reference's W8A16 tile
 // tables (src/ops/rpu_linear_tiling.h:69-127, selectors :544-595), but as
 // rules over (M, strips of 16 channels, 64-wide K blocks), tuned on MI355X:
@@ -1047,7 +1169,9 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
   const int cu = dev.cus > 0 ? dev.cus : 256;
   auto strips_ge = [&](int n256) { return (int64_t)nstrips * 256 >= (int64_t)n256 * cu; };
   int cfg, splits = 1;
-  if (M <= 16 && !strips_ge(640) && kblocks >= 256) {
+  if (int8_rules && plan_int8_rules(M, nstrips, kblocks, cu, &cfg, &splits)) {
+    // (measured int8 rules above)
+  } else if (M <= 16 && !strips_ge(640) && kblocks >= 256) {
     // Very long K (>= 16384) on few strips (Qwen3-VL-32B down_proj): two
     // strips per 8-wavefront workgroup and an 8-way K split.
     cfg = kG1x2W8U2;
@@ -1068,11 +1192,8 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
     } else if (kblocks >= 128 || (M == 1 && kblocks >= 80)) {
       // (at M = 1 from K = 5120: ten tiles per wavefront instead of five,
       // Qwen3-VL-32B k/v 1024 x 5120 4.84 instead of 5.15 us).  x is staged
-      // in LDS at M = 1, and for int8 at M = 2 from K 8192 too (Qwen3-8B down
-      // 4096 x 12288 at M = 2: 10.1..10.5 against 10.7..11.8 us, three
-      // rounds, graph-timed, 600 MB of rotated weights).
-      const bool xl = M == 1 || (int8_rules && M == 2 && kblocks >= 128);
-      cfg = (xl && lds_fits(kG1x1W8U4XL, M, kblocks)) ? kG1x1W8U4XL : kG1x1W8U4;
+      // in LDS at M = 1.
+      cfg = (M == 1 && lds_fits(kG1x1W8U4XL, M, kblocks)) ? kG1x1W8U4XL : kG1x1W8U4;
     } else if (kblocks <= 16) {
       // K <= 1024: four wavefronts of four tiles, one pipeline stage each,
       // and a 4-way cross-wavefront sum instead of 16 (Qwen3-0.6B q/k/v
@@ -1088,9 +1209,8 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
     const int64_t spc = ((int64_t)nstrips + cu - 1) / cu;
     if (strips_ge(2048)) {
       // M 5..8 (rows 8..15 of the activation fragment repeat row M-1, so
-      // it costs less): three strips per workgroup (Qwen3-14B lm_head
-      // 151936 x 5120 at M 8: 117.9 instead of 119.6 us; 32768 x 4096:
-      // 23.3 instead of 25.1 us).
+      // it costs less): three strips per workgroup (32768 x 4096: 23.3
+      // instead of 25.1 us); int8 from K 1088 in plan_int8_rules.
       cfg = (int8_rules && M <= 8) ? kG1x3W8U2 : kG1x4W4U2;
     } else if (int8_rules && strips_ge(1025) && spc <= 7) {
       // 5..7 strips per CU: that many strips per 8-wave workgroup, one

@@ -15,29 +15,54 @@ GEMV_POLICY = [
     # M 3..4, >=640 strips: two strips per 8-wave workgroup
     (3, 16384, 512, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     (4, 10240, 8256, "gemv 1x2 strips, 8 waves", 16, 32, 1),  # the same at long K
-    # M<=4, 257..639 strips: two strips per workgroup
+    # M<=4, 257..639 strips, K <= 1024: two strips per 16-wave workgroup
     (1, 5000, 320, "gemv 1x2 strips, 16 waves", 16, 32, 1),
-    # M=1, long K: x in LDS, 8 wavefronts
+    # M<=4, 257..639 strips from K 1088 (int8): two strips per 8-wave workgroup
+    (1, 8192, 5120, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    (3, 6144, 2560, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    (1, 5120, 16384, "gemv 1x2 strips, 8 waves", 16, 32, 1),   # very long K: no split
+    # ... except M<=2 at K 8192..16383: x in LDS
+    (1, 5120, 8192, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # M<=4, < 257 strips (int8): x in LDS, 8 wavefronts, at M 1..2
     (1, 512, 8192, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
-    # M<=4, long K: 8 wavefronts, x from global memory
-    (3, 512, 8192, "gemv 1x1 strips, 8 waves", 16, 16, 1),
-    # the same at M=2 from K 8192: x in LDS (int8)
     (2, 4096, 12288, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
-    # M=1, default: x in LDS, 16 wavefronts
+    (1, 512, 2048, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # same, x copy ends mid-way through a 1 KB DMA chunk
+    (1, 300, 3136, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # same, K % 64 != 0: x staged through registers, zero past K
+    (1, 520, 3080, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # at M 3 below 256 strips and M 4 up to 128
+    (3, 512, 8192, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    (4, 2048, 6144, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    # with a 2-way K split where only that fits in LDS (up to 128 strips)
+    (3, 2048, 11008, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 2),
+    (4, 2000, 10000, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 2),  # ragged N and K
+    # M 3..4 otherwise: 16 wavefronts (long K included)
+    (4, 2560, 4096, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    (4, 4096, 12288, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    (3, 4096, 2048, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # M 2..4 from K 16384 without room for x: two strips, about one workgroup per CU
+    (2, 3584, 18944, "gemv 1x2 strips, 8 waves", 16, 32, 2),
+    (4, 2048, 16384, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    # M=1, K 4096..5119 on <= 64 strips: x in LDS, 16 wavefronts
     (1, 512, 4096, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
     # same, x copy ends mid-way through a 1 KB DMA chunk
-    (1, 300, 3136, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    (1, 300, 4160, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
     # same, K % 64 != 0: x staged through registers, zero past K
-    (1, 520, 3080, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    (1, 520, 4104, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
     # M<=4, K <= 1024: four wavefronts of four tiles
     (1, 3072, 1024, "gemv 1x1 strips, 4 waves", 16, 16, 1),
     (4, 512, 1000, "gemv 1x1 strips, 4 waves", 16, 16, 1),   # ragged K (16 blocks)
     # M=1, 80..127 K blocks: x in LDS, 8 wavefronts
     (1, 1024, 5120, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
-    # M<=4, default (short K, or M > 1)
-    (1, 512, 2048, "gemv 1x1 strips, 16 waves", 16, 16, 1),
-    # M 9..16, >=2048 strips
+    # M 9..16, >=2048 strips, K < 3072
     (12, 32768, 128, "gemv 1x4 strips, 4 waves", 16, 64, 1),
+    # the same from K 3072 (int8): five strips per 8-wave workgroup
+    (12, 32768, 3072, "gemv 1x5 strips, 8 waves", 16, 80, 1),
+    # M 5..8, >=2048 strips from K 1088 (int8): three or five strips, the
+    # fuller rounds of workgroups (2368 strips: five)
+    (6, 37888, 1088, "gemv 1x5 strips, 8 waves", 16, 80, 1),
+    (8, 34816, 1152, "gemv 1x3 strips, 8 waves", 16, 48, 1),     # 2176 strips: three
     # M 5..8, >=2048 strips: three strips per 8-wave workgroup
     (8, 32768, 128, "gemv 1x3 strips, 8 waves", 16, 48, 1),
     (5, 40016, 136, "gemv 1x3 strips, 8 waves", 16, 48, 1),    # ragged N (2501 strips), K tail
@@ -62,21 +87,28 @@ GEMV_POLICY = [
     (10, 5000, 512, "gemv 1x2 strips, 16 waves", 16, 32, 1),
     # the same from K 5120: two strips per 8-wave workgroup
     (16, 5120, 5120, "gemv 1x2 strips, 8 waves", 16, 32, 1),
-    # M 5..16, long K, 129..256 strips: two strips per workgroup, 2-way K split
+    # M 7..16, K 8192..16383, 129..256 strips: two strips per workgroup, 2-way K split
     (16, 4096, 12288, "gemv 1x2 strips, 8 waves", 16, 32, 2),
-    (5, 2056, 8200, "gemv 1x2 strips, 8 waves", 16, 32, 2),     # ragged N and K
-    # M 5..16, long K, fewer strips: 4-way K split
-    (16, 1024, 8192, "gemv 1x4 strips, 8 waves", 16, 64, 4),
-    # M 5..16, <=64 strips: 4-way K split
-    (9, 1000, 1024, "gemv 1x2 strips, 16 waves", 16, 32, 4),
+    (7, 2056, 8200, "gemv 1x2 strips, 8 waves", 16, 32, 2),     # ragged N and K
+    # M 5..6 (int8): one strip per 16-wave workgroup, no split
+    (5, 2056, 8200, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # M 5..16, K 8192..16383, up to 128 strips (int8): two strips, 4-way K split
+    (16, 1024, 8192, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    # M 5..16 from K 16384 (int8): 4-way K split with five strips per
+    # workgroup on 257..511 strips, four on 129..256, two on fewer
+    (16, 4112, 16456, "gemv 1x5 strips, 8 waves", 16, 80, 4),  # ragged N and K
+    (8, 3584, 18944, "gemv 1x4 strips, 8 waves", 16, 64, 4),
+    (5, 2048, 16384, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    # M 5..16, <=64 strips (int8): one strip per 16-wave workgroup, no split
+    (9, 1000, 1024, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    (16, 1024, 2048, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # at M >= 8 from K 5120: one strip per 8-wave workgroup, 4-way K split
+    (12, 1024, 5120, "gemv 1x1 strips, 8 waves", 16, 16, 4),
     # M 5..16, default
     (16, 2048, 1024, "gemv 1x1 strips, 16 waves", 16, 16, 1),
-    # M <= 16, < 640 strips, K >= 16384: 2 strips per workgroup, 8-way split
-    (1, 5120, 16384, "gemv 1x2 strips, 8 waves", 16, 32, 8),
-    (16, 4112, 16456, "gemv 1x2 strips, 8 waves", 16, 32, 8),  # at M 16, ragged N and K
-    # M <= 2, 257..639 strips, K >= 5120: x in LDS
-    (1, 8192, 5120, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
-    # M 3..4, the same strips and K: 2 strips per workgroup
+    # M <= 16, 512..639 strips, K >= 16384: 2 strips per workgroup, 8-way split
+    (1, 8192, 16384, "gemv 1x2 strips, 8 waves", 16, 32, 8),
+    # M 3..4, 257..639 strips, long K: 2 strips per workgroup
     (4, 5120, 8192, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     # M 5..16, 512 strips (two per CU): 2 strips per workgroup
     (12, 8192, 512, "gemv 1x2 strips, 8 waves", 16, 32, 1),

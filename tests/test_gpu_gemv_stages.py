@@ -41,18 +41,19 @@ INT8_CASES = [
     # x in LDS, W=8 U=4, 131 K blocks: waves 0-2 run 17 tiles (5 stages, the
     # last of one tile), the rest 16 (4 full stages)
     (1, 512, 8384, "gemv 1x1 strips, 8 waves, x in LDS", 1, "5 / 4"),
-    # x from global, K tail (K % 64 = 8), W=8 U=4, 129 blocks: 17 / 16 tiles
-    (4, 512, 8200, "gemv 1x1 strips, 8 waves", 1, "5 / 4"),
+    # x in LDS with a 2-way K split (65 + 64 blocks, the K tail, K % 64 = 8,
+    # in the second), W=8 U=4: 9 / 8 tiles in the first split, 8 in the second
+    (4, 512, 8200, "gemv 1x1 strips, 8 waves, x in LDS", 2, "3 / 2"),
     # two strips, W=8 U=2, 2-way K split of 197 blocks (99 + 98): 13 / 12 tiles
     (16, 4096, 12608, "gemv 1x2 strips, 8 waves", 2, "7 / 6"),
     # x in LDS, 80 blocks over 8 waves: 10 tiles = 4 + 4 + 2
-    (1, 5120, 5120, "gemv 1x1 strips, 8 waves, x in LDS", 1, "3"),
+    (1, 4096, 5120, "gemv 1x1 strips, 8 waves, x in LDS", 1, "3"),
     # two strips, W=8 U=2, 81 blocks: wave 0 11 tiles (6 stages, last partial), the rest 10 (5)
     (16, 5120, 5184, "gemv 1x2 strips, 8 waves", 1, "6 / 5"),
     # three strips, W=8 U=2, 64 blocks: 8 tiles, 4 stages
     (8, 24576, 4096, "gemv 1x3 strips, 8 waves", 1, "4"),
-    # W=16 U=2, ragged N (63 strips, the last partial) and K tail, 66 blocks: 5 / 4 tiles
-    (3, 1000, 4168, "gemv 1x1 strips, 16 waves", 1, "3 / 2"),
+    # W=16 U=2, ragged N (256 strips, the last partial) and K tail, 66 blocks: 5 / 4 tiles
+    (3, 4090, 4168, "gemv 1x1 strips, 16 waves", 1, "3 / 2"),
 ]
 
 
