@@ -578,6 +578,68 @@ def bench_few_tiles(torch, rf):
     return rows
 
 
+# Decode projections of the reference's model families (hidden / q / k,v /
+# MLP widths from each model's config), q/k/v and gate/up fused as a decoder
+# layer issues them: (family, projection, output widths, K).
+MODEL_SHAPES = [
+    ("Qwen3-0.6B", "qkv", [2048, 1024, 1024], 1024), ("Qwen3-0.6B", "o", [1024], 2048),
+    ("Qwen3-0.6B", "gate_up", [3072, 3072], 1024), ("Qwen3-0.6B", "down", [1024], 3072),
+    ("Qwen3-1.7B", "qkv", [2048, 1024, 1024], 2048), ("Qwen3-1.7B", "o", [2048], 2048),
+    ("Qwen3-1.7B", "gate_up", [6144, 6144], 2048), ("Qwen3-1.7B", "down", [2048], 6144),
+    ("Qwen3-4B", "qkv", [4096, 1024, 1024], 2560), ("Qwen3-4B", "o", [2560], 4096),
+    ("Qwen3-4B", "gate_up", [9728, 9728], 2560), ("Qwen3-4B", "down", [2560], 9728),
+    ("Qwen3-8B", "qkv", [4096, 1024, 1024], 4096), ("Qwen3-8B", "o", [4096], 4096),
+    ("Qwen3-8B", "gate_up", [12288, 12288], 4096), ("Qwen3-8B", "down", [4096], 12288),
+    ("Qwen3-14B", "qkv", [5120, 1024, 1024], 5120), ("Qwen3-14B", "o", [5120], 5120),
+    ("Qwen3-14B", "gate_up", [17408, 17408], 5120), ("Qwen3-14B", "down", [5120], 17408),
+    ("Qwen3-(VL-)32B", "qkv", [8192, 1024, 1024], 5120), ("Qwen3-(VL-)32B", "o", [5120], 8192),
+    ("Qwen3-(VL-)32B", "gate_up", [25600, 25600], 5120), ("Qwen3-(VL-)32B", "down", [5120], 25600),
+    ("Qwen2.5-VL-3B", "qkv", [2048, 256, 256], 2048), ("Qwen2.5-VL-3B", "o", [2048], 2048),
+    ("Qwen2.5-VL-3B", "gate_up", [11008, 11008], 2048), ("Qwen2.5-VL-3B", "down", [2048], 11008),
+    ("Qwen2.5-VL-7B", "qkv", [3584, 512, 512], 3584), ("Qwen2.5-VL-7B", "o", [3584], 3584),
+    ("Qwen2.5-VL-7B", "gate_up", [18944, 18944], 3584), ("Qwen2.5-VL-7B", "down", [3584], 18944),
+    ("Pi0.5 Gemma 2B", "qkv", [2048, 256, 256], 2048), ("Pi0.5 Gemma 2B", "o", [2048], 2048),
+    ("Pi0.5 Gemma 2B", "gate_up", [16384, 16384], 2048), ("Pi0.5 Gemma 2B", "down", [2048], 16384),
+    ("Pi0.5 expert", "qkv", [2048, 256, 256], 1024), ("Pi0.5 expert", "o", [1024], 2048),
+    ("Pi0.5 expert", "gate_up", [4096, 4096], 1024), ("Pi0.5 expert", "down", [1024], 4096),
+]
+MODEL_SHAPES_M = (1, 4, 8, 16)
+
+
+def bench_model_shapes(torch, rf):
+    """Per-launch times of MODEL_SHAPES at M in MODEL_SHAPES_M through
+    linear_into / linear_multi (AUTO), replayed from a HIP graph, rotating
+    weight copies of >= 320 MB per shape (random int8 tiles: the timing does
+    not depend on the values), against HBM."""
+    from rhinoforge_amd import capi
+    from rhinoforge_amd.ops import packed_shape
+    rows = []
+    for fam, proj, ns, k in MODEL_SHAPES:
+        wbytes = sum(n * k for n in ns)
+        ncopies = max(4, -(-(320 << 20) // wbytes))
+        cs = [[torch.randint(-127, 128, packed_shape(n, k), dtype=torch.int8, device="cuda")
+               for n in ns] for _ in range(ncopies)]
+        sc = [torch.full((n,), 1e-3, dtype=torch.float16, device="cuda") for n in ns]
+        for m in MODEL_SHAPES_M:
+            x = torch.randn(m, k, device="cuda").half()
+            if len(ns) == 1:
+                y = torch.empty(m, ns[0], device="cuda", dtype=torch.float16)
+                fn = lambda c: rf.linear_into(x, c[0], sc[0], None, y)  # noqa: E731
+            else:
+                fn = lambda c: rf.linear_multi(x, c, sc)  # noqa: E731
+            us = per_launch_us(torch, fn, cs, max(2 * ncopies, 48))
+            p = capi.plan(m, ns, k)
+            b = sum(nbytes(m, n, k) for n in ns) - (len(ns) - 1) * 2 * m * k
+            rows.append(roofline_row({"family": fam, "proj": proj, "M": m, "N": ns, "K": k,
+                                      "us": round(us, 2),
+                                      "plan": f"{p['name']}, {p['splits']} split(s)"},
+                                     "hbm", b, 2 * m * sum(ns) * k))
+        log(f"  {fam} {proj}: " + ", ".join(f"M{r['M']} {r['us']}" for r in rows[-len(MODEL_SHAPES_M):]))
+        del cs
+        torch.cuda.empty_cache()
+    return rows
+
+
 def bench_other_configs(torch, rf):
     """Per-launch timings of BASELINE configs 0, 2 and 4 and the W4A16 rows (not
     part of `value`); returns them and config 2's argmax case for cpu_baseline."""
@@ -804,7 +866,7 @@ def main():
                     help="first run three device-to-device copies of this many MB (the "
                          "known-size reference kernel for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--only", choices=("decode", "prefill", "cfg0", "cfg2", "cfg4", "w4a16",
-                                       "few_tiles"),
+                                       "few_tiles", "model_shapes"),
                     help="run one section alone and print its result (a profiling aid: "
                          "its JSON line is not the benchmark line)")
     args = ap.parse_args()
@@ -841,6 +903,7 @@ def main():
             "cfg4": lambda: bench_cfg4(torch, rf),
             "w4a16": lambda: bench_w4a16(torch, rf),
             "few_tiles": lambda: bench_few_tiles(torch, rf),
+            "model_shapes": lambda: bench_model_shapes(torch, rf),
         }
         print(json.dumps({"only": args.only, "result": sections[args.only]()}), flush=True)
         return
