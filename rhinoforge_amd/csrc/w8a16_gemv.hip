@@ -959,6 +959,35 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
 //     group-wise alike: 12288 x 4096 at M 5..16 7.3..9.1 against
 //     8.8..9.7 us; 24576 x 4096 at M 16 13.7 against 16.4 us, at M 8 12.3
 //     against 14.1 us; 25600 x 5120 at M 16 19.1 against 20.8 us).
+// Ahead of those, rules measured over the decode projections of the
+// reference's model families (Qwen3 0.6B..32B, Qwen3-VL-32B, Qwen2.5-VL
+// 3B / 7B, the Pi0.5 Gemma decoder and expert) at M 1 / 2 / 4 / 8 / 16,
+// per-channel and group-wise (128), against every configuration and K
+// split; checked against the rules above on the 80 launches they change:
+// 0.884 of the time (geometric mean), worst +1.7%:
+//   * M 2..4 on >= 1024 strips from 24 tiles, and M 1 at 24..39 tiles: two
+//     strips per 8-wave workgroup instead of x in LDS (Qwen3-8B gate/up
+//     24576 x 4096 at M 4: 12.5 against 13.7 us per-channel, 12.8 against
+//     16.2 us group-wise);
+//   * M 2..4 from 128 tiles below 257 strips: two strips per workgroup,
+//     split to about one workgroup per CU (Pi0.5 Gemma down 2048 x 16384 at
+//     M 4: 8.0 against 10.6 us);
+//   * per-channel M <= 2 at 64..127 tiles below 257 strips: x in LDS with 8
+//     wavefronts instead of 16 (Qwen3-8B down 4096 x 12288 at M 1: 6.7
+//     against 7.4 us);
+//   * M 8..16 on >= 2048 strips: four strips per 8-wave workgroup, or three
+//     or seven where they keep the rounds of 256 workgroups more than 5%
+//     fuller, where one of them fills 85% (Qwen3-14B gate/up 34816 x 5120 at
+//     M 8: three, 19.6 against 22.3 us);
+//   * M 8..16 on <= 128 strips from 64 tiles (48 from M 12): two strips,
+//     4-way split (Pi0.5 Gemma down at M 16: 9.6 against 11.1 us);
+//     M 12..16 on 129..256 strips from 64 tiles: four strips, 4-way split;
+//   * M 8..16 on 257..511 strips from 128 tiles: three strips and a 2-way
+//     split at M 8, six strips and a 4-way split above (Qwen3-VL-32B down
+//     5120 x 25600 at M 16: 19.8 against 24.2 us);
+//   * M 9..16 on <= 64 strips below 32 tiles: one strip per 16-wave
+//     workgroup, no split (Pi0.5 expert o 1024 x 2048 at M 16: 4.2 against
+//     5.4 us).
 GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
                         const DeviceInfo& dev) {
   const int keff = (int)(round_up(K, kTileK4) / 2);
@@ -972,7 +1001,46 @@ GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
   auto fits_xl = [&](int w) { return gemv_lds_bytes(1, 1, w, true, M, ktiles, kTileK4) <= 65536; };
   int cfg = p.cfg, splits = p.splits;
   const int64_t spc = ((int64_t)nstrips + cu - 1) / cu;  // strips per CU, rounded up
-  if (M >= 5 && M <= 16 && p.splits == 1 && strips_ge(513) && (spc == 3 || spc == 6 || spc == 7)) {
+  auto groups = [&](int ns) { return (nstrips + ns - 1) / ns; };
+  // M 8..16 on >= 2048 strips: four strips per 8-wave workgroup unless three
+  // or seven keep the rounds of `cu` workgroups more than 5% fuller; -1
+  // (the rules below) where none fills them to 85%.
+  int many_strips_cfg = -1;
+  if (M >= 8 && M <= 16 && strips_ge(2048)) {
+    auto fill = [&](int ns) {
+      const int g = groups(ns);
+      return (double)g / (double)(((g + cu - 1) / cu) * cu);
+    };
+    int c = kG1x4W8U2;
+    double best = fill(4) * 1.05;
+    if (fill(3) > best) { c = kG1x3W8U2; best = fill(3); }
+    if (fill(7) > best) c = kG1x7W8U1;
+    if (std::max(fill(4), std::max(fill(3), fill(7))) >= 0.85) many_strips_cfg = c;
+  }
+  if (M <= 4 && strips_ge(1024) && ktiles >= 24 && (M >= 2 || ktiles < 40)) {
+    cfg = kG1x2W8U2;
+    splits = 1;
+  } else if (M >= 2 && M <= 4 && ktiles >= 128 && !strips_ge(257)) {
+    cfg = kG1x2W8U2;
+    splits = std::max(1, std::min(8, (cu + groups(2) / 2) / groups(2)));
+  } else if (!grouped && M <= 2 && !strips_ge(257) && ktiles >= 64 && ktiles < 128 && fits_xl(8)) {
+    cfg = kG1x1W8U4XL;
+  } else if (many_strips_cfg >= 0) {
+    cfg = many_strips_cfg;
+    splits = 1;
+  } else if (M >= 8 && M <= 16 && (ktiles >= 64 || (M >= 12 && ktiles >= 48)) && !strips_ge(129)) {
+    cfg = kG1x2W8U2;
+    splits = 4;
+  } else if (M >= 12 && M <= 16 && ktiles >= 64 && strips_ge(129) && !strips_ge(257)) {
+    cfg = kG1x4W8U2;
+    splits = 4;
+  } else if (M >= 8 && M <= 16 && ktiles >= 128 && strips_ge(257) && !strips_ge(512)) {
+    cfg = M <= 8 ? kG1x3W8U2 : kG1x6W8U1;
+    splits = M <= 8 ? 2 : 4;
+  } else if (M >= 9 && M <= 16 && !strips_ge(65) && ktiles < 32) {
+    cfg = kG1x1W16U2;
+    splits = 1;
+  } else if (M >= 5 && M <= 16 && p.splits == 1 && strips_ge(513) && (spc == 3 || spc == 6 || spc == 7)) {
     cfg = spc == 3 ? kG1x3W8U2 : spc == 7 ? kG1x7W8U1 : M >= 12 ? kG1x6W8U1 : kG1x3W8U2;
   } else if (M <= 4 && p.splits == 1 && !strips_ge(257) && ktiles < 128) {
     // Below 64 tiles the x copy (at most 4 rows of 63 * 256 bytes) fits.

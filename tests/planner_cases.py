@@ -150,7 +150,9 @@ GEMV_INT4_POLICY = [
     (2, 1024, 5120, True, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
     (2, 1024, 4096, True, "gemv 1x1 strips, 16 waves", 16, 16, 1),
     # 64..127 tiles, M <= 3: x in LDS, 16 wavefronts, where the copy fits
-    (2, 4096, 12288, False, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
+    # (per-channel at M <= 2: 8 wavefronts)
+    (2, 4096, 12288, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
+    (3, 4096, 8192, False, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
     (2, 1008, 16256, True, "gemv 1x1 strips, 16 waves, x in LDS", 16, 16, 1),
     (3, 4096, 12288, True, "gemv 1x1 strips, 16 waves", 16, 16, 1),
     # M = 4 from 64 tiles: the int8 rule
@@ -163,10 +165,37 @@ GEMV_INT4_POLICY = [
     (2, 5120, 25600, False, "gemv 1x2 strips, 16 waves", 16, 32, 1),
     # M 3..4, >= 640 strips: x in LDS (int8 takes two strips per workgroup)
     (4, 12288, 4096, True, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
-    # M 8..16, >= 1793 strips: four strips per 4-wave workgroup; M 5..7 at
-    # 1025..1280 strips keeps two
-    (8, 32768, 4096, False, "gemv 1x4 strips, 4 waves", 16, 64, 1),
+    # M 8..16, >= 2048 strips: four strips per 8-wave workgroup, or three /
+    # seven where they fill the rounds of workgroups more than 5% better
+    (8, 32768, 4096, False, "gemv 1x4 strips, 8 waves", 16, 64, 1),
+    (16, 34816, 1024, True, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    (12, 51200, 1024, False, "gemv 1x7 strips, 8 waves", 16, 112, 1),
+    # ... and where none fills them to 85% (2368 strips), or at 1793..2047
+    # strips: four strips per 4-wave workgroup; M 5..7 at 1025..1280 strips
+    # keeps two
+    (16, 37888, 1024, True, "gemv 1x4 strips, 4 waves", 16, 64, 1),
+    (8, 31744, 1024, False, "gemv 1x4 strips, 4 waves", 16, 64, 1),
     (5, 20480, 4096, False, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 2..4 on >= 1024 strips from 24 tiles (M 1 below 40): two strips per
+    # 8-wave workgroup
+    (2, 24576, 4096, False, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    (1, 24576, 4096, True, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 2..4 from 128 tiles below 257 strips: two strips, split to about one
+    # workgroup per CU
+    (4, 2048, 16384, False, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    (2, 3584, 18944, True, "gemv 1x2 strips, 8 waves", 16, 32, 2),
+    # M 8..16 on <= 128 strips from 64 tiles (48 from M 12): two strips,
+    # 4-way K split
+    (8, 2048, 11008, False, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    (12, 2048, 6144, True, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    # M 12..16 on 129..256 strips from 64 tiles: four strips, 4-way K split
+    (16, 2560, 9728, False, "gemv 1x4 strips, 8 waves", 16, 64, 4),
+    # M 8..16 on 257..511 strips from 128 tiles: three strips and a 2-way
+    # split at M 8, six strips and a 4-way split above
+    (8, 5120, 17408, False, "gemv 1x3 strips, 8 waves", 16, 48, 2),
+    (16, 5120, 25600, True, "gemv 1x6 strips, 8 waves", 16, 96, 4),
+    # M 9..16 on <= 64 strips below 32 tiles: one strip, no split
+    (12, 1024, 2048, False, "gemv 1x1 strips, 16 waves", 16, 16, 1),
     # M 5..16, 3 / 6 / 7 strips per CU: that many strips per 8-wave
     # workgroup (three at 6 per CU below M 12)
     (5, 12288, 4096, True, "gemv 1x3 strips, 8 waves", 16, 48, 1),
@@ -180,8 +209,8 @@ GEMV_INT4_POLICY = [
     # the same strips at 64..127 tiles: two strips per 8-wave workgroup from M 8
     (8, 5120, 8192, True, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     (5, 5120, 8192, True, "gemv 1x2 strips, 16 waves", 16, 32, 1),
-    # M 5..16, >= 64 tiles on < 257 strips: two strips per workgroup, 2-way K split
-    (16, 4096, 12288, True, "gemv 1x2 strips, 8 waves", 16, 32, 2),
+    # M 5..11, >= 64 tiles on 129..256 strips: two strips per workgroup, 2-way K split
+    (8, 4096, 12288, True, "gemv 1x2 strips, 8 waves", 16, 32, 2),
     # M 5..8, <= 64 strips: no K split (int8 splits 4 ways); from M 9 the split
     (8, 1024, 4096, False, "gemv 1x1 strips, 16 waves", 16, 16, 1),
     (12, 1024, 4096, False, "gemv 1x2 strips, 16 waves", 16, 32, 4),

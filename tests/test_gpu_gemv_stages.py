@@ -81,14 +81,18 @@ def test_int8_stage_counts(case):
 
 # (M, N, K, group size (0: per channel), plan name, K splits, stages per wavefront).
 INT4_CASES = [
-    # per-channel, x in LDS, W=16 U=2, 96 int4 tiles: 6 tiles, 3 stages
-    (1, 4096, 12288, 0, "gemv 1x1 strips, 16 waves, x in LDS", 1, "3"),
+    # per-channel, x in LDS, W=8 U=2, 96 int4 tiles: 12 tiles, 6 stages
+    (1, 4096, 12288, 0, "gemv 1x1 strips, 8 waves, x in LDS", 1, "6"),
+    # per-channel, x in LDS, W=16 U=2 at M 3, 64 tiles: 4 tiles, 2 stages
+    (3, 4096, 8192, 0, "gemv 1x1 strips, 16 waves, x in LDS", 1, "2"),
     # group-wise 32, W=8 U=1, 2-way split of 96 tiles: 6 tiles, 6 stages of one
-    (16, 4096, 12288, 32, "gemv 1x2 strips, 8 waves", 2, "6"),
+    (8, 4096, 12288, 32, "gemv 1x2 strips, 8 waves", 2, "6"),
+    # group-wise 32, four strips, W=8 U=1, 4-way split of 96 tiles: 3 tiles, 3 stages
+    (16, 4096, 12288, 32, "gemv 1x4 strips, 8 waves", 4, "3"),
     # group-wise 128, x in LDS, W=16 U=1: 6 stages of one tile
     (2, 4096, 12288, 128, "gemv 1x1 strips, 16 waves, x in LDS", 1, "6"),
-    # per-channel, 16 waves U=1, 4-way split of 65 tiles (17/17/17/14), K % 128 = 64
-    (16, 1008, 8256, 0, "gemv 1x2 strips, 16 waves", 4, "2 / 1"),
+    # per-channel, W=8 U=1, 4-way split of 65 tiles (17/17/17/14), K % 128 = 64: 3 / 2 tiles
+    (16, 1008, 8256, 0, "gemv 1x2 strips, 8 waves", 4, "3 / 2"),
 ]
 
 
