@@ -144,15 +144,19 @@ int check_nk(int64_t N, int64_t K) {
 }
 
 // Kernel the AUTO policy picks (N summed over a launch's projections).
-// Measured on MI355X over the Qwen3-8B and Qwen3-VL-32B projections: the
-// GEMV wins up to M = 16; from M = 17 the small-tile split-K GEMM wins on
-// every shape but small weights, where the GEMV keeps a ~1 us lead (N*K <=
-// 2^24 up to M = 28, N*K <= 2^23 up to M = 32).  The GEMV runs up to M = 64
-// when forced.
+// Measured on MI355X over the projections of Qwen3 0.6B..32B, Qwen3-VL-32B,
+// Qwen2.5-VL 3B / 7B and the Pi0.5 Gemma decoder and expert (each alone and
+// q/k/v, gate/up fused): the GEMV wins up to M = 16; from M = 17 the
+// small-tile split-K GEMM wins on every shape but small weights, where the
+// GEMV keeps its lead: N*K < 2^25 up to M = 24 (Qwen3-8B q/k/v 6144 x 4096
+// at M 24: 10.4 against 12.2 us), N*K <= 2^24 up to M = 28, and up to M = 32
+// N*K <= 2^23, or N*K <= 2^24 on N <= 2048 (Qwen3-1.7B down 2048 x 6144 at
+// M 32: 9.0 against 12.5 us).  The GEMV runs up to M = 64 when forced.
 int auto_kernel(int64_t M, int64_t N, int64_t K) {
   if (M <= 16) return RF_W8A16_KERNEL_GEMV;
   const int64_t nk = N * K;
-  if ((M <= 28 && nk <= ((int64_t)1 << 24)) || (M <= 32 && nk <= ((int64_t)1 << 23)))
+  if ((M <= 24 && nk < ((int64_t)1 << 25)) || (M <= 28 && nk <= ((int64_t)1 << 24)) ||
+      (M <= 32 && (nk <= ((int64_t)1 << 23) || (N <= 2048 && nk <= ((int64_t)1 << 24)))))
     return RF_W8A16_KERNEL_GEMV;
   return RF_W8A16_KERNEL_GEMM;
 }

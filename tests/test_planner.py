@@ -63,6 +63,10 @@ BASELINE_LAUNCHES = [
     ((2048, [4096], 12288), "gemm"),               # cfg3 down
     ((1, [25600, 25600], 5120), "gemv"),           # cfg4 at M 1 / 32 / 512
     ((32, [1024], 5120), "gemv"),                  # k/v at M 32: small weight, GEMV
+    ((24, [4096, 1024, 1024], 4096), "gemv"),      # N*K < 2^25 up to M 24
+    ((28, [4096, 1024, 1024], 4096), "gemm"),
+    ((32, [2048], 6144), "gemv"),                  # N <= 2048, N*K <= 2^24 at M 32
+    ((32, [4096], 4096), "gemm"),
     ((32, [8192], 5120), "gemm"),                  # q at M 32: mid-M GEMM tiles
     ((32, [5120], 25600), "gemm"),
     ((512, [8192, 1024, 1024], 5120), "gemm"),
