@@ -1326,11 +1326,37 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
       cfg = kG1x1W16U2;
     }
   } else if (M <= 32) {
+    // int8 below 640 strips, measured over the projections of the model
+    // families that stay on the GEMV at M 17..32 (graph-timed, 600 MB of
+    // rotated weights): from K 8192 on <= 256 strips, two strips per
+    // 16-wavefront workgroup split 4-way (<= 128 strips) or 2-way
+    // (Qwen2.5-VL-3B down 2048 x 11008 at M 24: 10.7 against 16.7 us;
+    // Qwen3-4B down 2560 x 9728: 13.7 against 15.9 us); at K 3072..8191 on
+    // 129..256 strips the same 2-way (Qwen3-8B o at M 24: 8.7 against
+    // 9.7 us); below K 3072 one strip per 8-wavefront workgroup of four
+    // tiles a stage on 65..256 strips (Pi0.5 Gemma 2B q/k/v 2560 x 2048 at
+    // M 24: 5.8 against 6.4 us), two strips per 16-wavefront workgroup on
+    // 257..639 (Qwen3-0.6B gate/up 6144 x 1024: 4.8 against 5.0 us), and no
+    // K split on <= 64 strips up to M 24 and K 2048 (Qwen3-0.6B o 1024 x
+    // 2048: 5.7 against 6.1 us).
+    const bool k_short = kblocks < 48;
     if (strips_ge(1024)) {
       cfg = kG2x4W4U2;
+    } else if (int8_rules && kblocks >= 128 && !strips_ge(257)) {
+      cfg = kG2x2W16U1;
+      splits = strips_ge(129) ? 2 : 4;
     } else if (kblocks >= 128) {
       cfg = kG2x4W4U2;
       splits = 4;
+    } else if (int8_rules && strips_ge(129) && !strips_ge(257) && !k_short) {
+      cfg = kG2x2W16U1;
+      splits = 2;
+    } else if (int8_rules && strips_ge(65) && !strips_ge(257) && k_short) {
+      cfg = kG2x1W8U4;
+    } else if (int8_rules && strips_ge(257) && !strips_ge(640) && k_short) {
+      cfg = kG2x2W16U1;
+    } else if (int8_rules && !strips_ge(65) && kblocks <= 32 && M <= 24) {
+      cfg = kG2x1W8U4;
     } else if (int8_rules && !strips_ge(129) && kblocks >= 64) {
       // <= 128 strips, K 4096..8191 (int8): two strips per 16-wavefront
       // workgroup and a 4-way K split (MI355X, 600 MB of rotated weights:

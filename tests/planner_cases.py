@@ -114,16 +114,27 @@ GEMV_POLICY = [
     (12, 8192, 512, "gemv 1x2 strips, 8 waves", 16, 32, 1),
     # M 17..32, >=1024 strips
     (20, 16384, 128, "gemv 2x4 strips, 4 waves", 32, 64, 1),
-    # M 17..32, long K: 4-way K split
-    (32, 640, 8192, "gemv 2x4 strips, 4 waves", 32, 64, 4),
+    # M 17..32, long K on 257..1023 strips: 4-way K split
+    (32, 4112, 8192, "gemv 2x4 strips, 4 waves", 32, 64, 4),
+    # ... on <= 256 strips (int8): two strips per 16-wave workgroup, 4-way
+    # split up to 128 strips, 2-way above
+    (32, 640, 8192, "gemv 2x2 strips, 16 waves", 32, 32, 4),
+    (24, 2560, 9728, "gemv 2x2 strips, 16 waves", 32, 32, 2),
     # M 17..32, <=128 strips, K 4096..8191 (int8): two strips per 16-wave workgroup, 4-way split
     (24, 1024, 4096, "gemv 2x2 strips, 16 waves", 32, 32, 4),
     (32, 2040, 5128, "gemv 2x2 strips, 16 waves", 32, 32, 4),  # ragged N and K
-    (17, 2064, 4096, "gemv 2x2 strips, 8 waves", 32, 32, 1),  # 129 strips: the default
-    # M 17..32, <=64 strips: 4-way K split
-    (17, 1024, 512, "gemv 2x1 strips, 8 waves", 32, 16, 4),
+    # 129..256 strips from K 3072 (int8): the same, 2-way split
+    (17, 2064, 4096, "gemv 2x2 strips, 16 waves", 32, 32, 2),
+    # below K 3072 (int8): one strip per 8-wave workgroup on 65..256 strips,
+    # two per 16-wave workgroup on 257..639
+    (24, 2048, 512, "gemv 2x1 strips, 8 waves", 32, 16, 1),
+    (24, 2560, 2048, "gemv 2x1 strips, 8 waves", 32, 16, 1),
+    (24, 6144, 1024, "gemv 2x2 strips, 16 waves", 32, 32, 1),
+    # M 17..32, <=64 strips: 4-way K split; no split up to M 24 and K 2048 (int8)
+    (32, 1024, 512, "gemv 2x1 strips, 8 waves", 32, 16, 4),
+    (17, 1024, 512, "gemv 2x1 strips, 8 waves", 32, 16, 1),
     # M 17..32, default
-    (24, 2048, 512, "gemv 2x2 strips, 8 waves", 32, 32, 1),
+    (24, 6144, 4096, "gemv 2x2 strips, 8 waves", 32, 32, 1),
     # M 33..64, >=512 strips
     (40, 8192, 256, "gemv 4x2 strips, 4 waves", 64, 32, 1),
     # M 33..64, default: 2-way K split
