@@ -987,7 +987,21 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
 //     5120 x 25600 at M 16: 19.8 against 24.2 us);
 //   * M 9..16 on <= 64 strips below 32 tiles: one strip per 16-wave
 //     workgroup, no split (Pi0.5 expert o 1024 x 2048 at M 16: 4.2 against
-//     5.4 us).
+//     5.4 us);
+//   * M 17..32 (int4 stays on the GEMV to M 64) below 1024 strips: two
+//     strips per 4-wave workgroup from 640 strips (Qwen3-VL-32B q/k/v 10240
+//     x 5120 at M 32: 17.8 against 27.8 us); on 65..256 strips one strip
+//     per 8-wave workgroup of four tiles a stage below 24 tiles, else two
+//     strips split 2-way (129..256, below 128 tiles) or 4-way (Qwen2.5-VL-3B
+//     down 2048 x 11008 at M 32: 11.9 against 26.3 us); on <= 64 strips no
+//     split up to M 24 below 24 tiles;
+//   * M 33..64: from 512 strips four strips per 4-wave workgroup (two per
+//     8-wave workgroup at <= 8 tiles), split 2-way on 512..767 strips from
+//     32 tiles; on 257..511 strips two strips per 8-wave workgroup without
+//     a split, or per 4-wave workgroup split 4-way from 128 tiles (Qwen3-14B
+//     q/k/v at M 48: 20.0 against 25.2 us; Qwen3-VL-32B down: 67.2 against
+//     85.2 us); below 257 strips a 4-way split up to 128 strips and none at
+//     <= 8 tiles (Qwen3-0.6B q/k/v 4096 x 1024 at M 48: 6.3 against 7.9 us).
 GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
                         const DeviceInfo& dev) {
   const int keff = (int)(round_up(K, kTileK4) / 2);
@@ -1017,7 +1031,37 @@ GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
     if (fill(7) > best) c = kG1x7W8U1;
     if (std::max(fill(4), std::max(fill(3), fill(7))) >= 0.85) many_strips_cfg = c;
   }
-  if (M <= 4 && strips_ge(1024) && ktiles >= 24 && (M >= 2 || ktiles < 40)) {
+  if (M >= 17 && M <= 32 && !strips_ge(1024)) {
+    // (two m-tiles per wavefront)
+    if (strips_ge(640)) {
+      cfg = kG2x4W4U2;
+      splits = 1;
+    } else if (strips_ge(257)) {
+      cfg = ktiles >= 128 ? kG2x4W4U2 : kG2x2W8U1;
+      splits = ktiles >= 128 ? 4 : 1;
+    } else if (strips_ge(129) && ktiles >= 128) {
+      cfg = kG2x4W4U2;
+      splits = 4;
+    } else if (strips_ge(65)) {
+      cfg = ktiles < 24 ? kG2x1W8U4 : kG2x2W8U1;
+      splits = ktiles < 24 ? 1 : strips_ge(129) ? 2 : 4;
+    } else {
+      cfg = kG2x1W8U4;
+      splits = M <= 24 && ktiles < 24 ? 1 : 4;
+    }
+  } else if (M >= 33 && M <= 64) {
+    // (four m-tiles per wavefront)
+    if (strips_ge(512)) {
+      cfg = ktiles <= 8 ? kG4x2W8U1 : kG4x2W4U1;
+      splits = !strips_ge(768) && ktiles >= 32 ? 2 : 1;
+    } else if (strips_ge(257)) {
+      cfg = ktiles >= 128 ? kG4x2W4U1 : kG4x2W8U1;
+      splits = ktiles >= 128 ? 4 : 1;
+    } else {
+      cfg = kG4x2W8U1;
+      splits = !strips_ge(129) ? 4 : ktiles <= 8 ? 1 : 2;
+    }
+  } else if (M <= 4 && strips_ge(1024) && ktiles >= 24 && (M >= 2 || ktiles < 40)) {
     cfg = kG1x2W8U2;
     splits = 1;
   } else if (M >= 2 && M <= 4 && ktiles >= 128 && !strips_ge(257)) {

@@ -207,6 +207,32 @@ GEMV_INT4_POLICY = [
     (16, 5120, 25600, True, "gemv 1x6 strips, 8 waves", 16, 96, 4),
     # M 9..16 on <= 64 strips below 32 tiles: one strip, no split
     (12, 1024, 2048, False, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # M 17..32 (int4 keeps the GEMV to M 64): four strips per 4-wave
+    # workgroup from 640 strips; on 257..639 two per 8-wave workgroup, split
+    # 4-way by 4 waves from 128 tiles
+    (32, 10240, 5120, False, "gemv 2x4 strips, 4 waves", 32, 64, 1),
+    (24, 6144, 4096, True, "gemv 2x2 strips, 8 waves", 32, 32, 1),
+    # 65..256 strips: one strip per 8-wave workgroup below 24 tiles, else two
+    # strips split 2-way (129..256, below 128 tiles) or 4-way
+    (24, 2048, 2048, False, "gemv 2x1 strips, 8 waves", 32, 16, 1),
+    (32, 2560, 9728, False, "gemv 2x2 strips, 8 waves", 32, 32, 2),
+    (32, 2048, 16384, True, "gemv 2x2 strips, 8 waves", 32, 32, 4),
+    (32, 3584, 18944, False, "gemv 2x4 strips, 4 waves", 32, 64, 4),
+    # <= 64 strips: no split up to M 24 below 24 tiles, else 4-way
+    (24, 1024, 2048, False, "gemv 2x1 strips, 8 waves", 32, 16, 1),
+    (32, 1024, 2048, True, "gemv 2x1 strips, 8 waves", 32, 16, 4),
+    # M 33..64: from 512 strips four strips per 4-wave workgroup (two per
+    # 8-wave workgroup at <= 8 tiles), 2-way split on 512..767 strips from 32 tiles
+    (48, 12288, 2048, False, "gemv 4x2 strips, 4 waves", 64, 32, 1),
+    (40, 10240, 5120, True, "gemv 4x2 strips, 4 waves", 64, 32, 2),
+    (48, 8192, 1024, False, "gemv 4x2 strips, 8 waves", 64, 32, 1),
+    # 257..511 strips: no split, or 4-wave and 4-way from 128 tiles
+    (48, 4096, 1024, False, "gemv 4x2 strips, 8 waves", 64, 32, 1),
+    (48, 5120, 17408, False, "gemv 4x2 strips, 4 waves", 64, 32, 4),
+    # below 257 strips: 4-way up to 128 strips, 2-way above (none at <= 8 tiles)
+    (64, 1024, 2048, False, "gemv 4x2 strips, 8 waves", 64, 32, 4),
+    (48, 4096, 4096, True, "gemv 4x2 strips, 8 waves", 64, 32, 2),
+    (33, 2560, 1024, False, "gemv 4x2 strips, 8 waves", 64, 32, 1),
     # M 5..16, 3 / 6 / 7 strips per CU: that many strips per 8-wave
     # workgroup (three at 6 per CU below M 12)
     (5, 12288, 4096, True, "gemv 1x3 strips, 8 waves", 16, 48, 1),
