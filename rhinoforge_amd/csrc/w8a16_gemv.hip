@@ -965,10 +965,18 @@ GemvPlan plan_gemv_rules(int M, const int* Ns, int nproj, int K, const DeviceInf
 // per-channel and group-wise (128), against every configuration and K
 // split; checked against the rules above on the 80 launches they change:
 // 0.884 of the time (geometric mean), worst +1.7%:
-//   * M 2..4 on >= 1024 strips from 24 tiles, and M 1 at 24..39 tiles: two
-//     strips per 8-wave workgroup instead of x in LDS (Qwen3-8B gate/up
-//     24576 x 4096 at M 4: 12.5 against 13.7 us per-channel, 12.8 against
-//     16.2 us group-wise);
+//   * M 2..4 on >= 1024 strips from 24 tiles (M 3..4 from 16), and M 1 at
+//     24..39 tiles: two strips per 8-wave workgroup instead of x in LDS
+//     (Qwen3-8B gate/up 24576 x 4096 at M 4: 12.5 against 13.7 us
+//     per-channel, 12.8 against 16.2 us group-wise);
+//   * M <= 4 on 257..511 strips from 128 tiles: x in LDS split 2-way (4-way
+//     from 192 tiles) at M <= 2, two strips split 4-way at M 3..4
+//     (Qwen3-VL-32B down 5120 x 25600 at M 2: 16.2 against 17.9 us); M 3..4
+//     on <= 128 strips from 64 tiles: two strips split 4-way (Qwen2.5-VL-3B
+//     down 2048 x 11008 at M 4: 7.2 against 8.0 us);
+//   * M 8..16 at five strips per CU (1025..1280 strips): three strips per
+//     workgroup, six from M 12 (Qwen3-4B gate/up 19456 x 2560 at M 16: 9.4
+//     against 11.7 us);
 //   * M 2..4 from 128 tiles below 257 strips: two strips per workgroup,
 //     split to about one workgroup per CU (Pi0.5 Gemma down 2048 x 16384 at
 //     M 4: 8.0 against 10.6 us);
@@ -1061,9 +1069,20 @@ GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
       cfg = kG4x2W8U1;
       splits = !strips_ge(129) ? 4 : ktiles <= 8 ? 1 : 2;
     }
-  } else if (M <= 4 && strips_ge(1024) && ktiles >= 24 && (M >= 2 || ktiles < 40)) {
+  } else if (M <= 4 && strips_ge(1024) &&
+             (ktiles >= 24 ? (M >= 2 || ktiles < 40) : (M >= 3 && ktiles >= 16))) {
     cfg = kG1x2W8U2;
     splits = 1;
+  } else if (M <= 4 && ktiles >= 128 && strips_ge(257) && !strips_ge(512)) {
+    // x in LDS split 2- or 4-way at M <= 2, two strips split 4-way at M 3..4
+    cfg = M <= 2 ? kG1x1W8U4XL : kG1x2W8U2;
+    splits = M <= 2 && ktiles < 192 ? 2 : 4;
+    if (cfg == kG1x1W8U4XL &&
+        gemv_lds_bytes(1, 1, 8, true, M, (int)ceil_div(ktiles, splits), kTileK4) > 65536)
+      cfg = kG1x2W8U2;
+  } else if (M >= 3 && M <= 4 && ktiles >= 64 && !strips_ge(129)) {
+    cfg = kG1x2W8U2;
+    splits = 4;
   } else if (M >= 2 && M <= 4 && ktiles >= 128 && !strips_ge(257)) {
     cfg = kG1x2W8U2;
     splits = std::max(1, std::min(8, (cu + groups(2) / 2) / groups(2)));
@@ -1084,7 +1103,8 @@ GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
   } else if (M >= 9 && M <= 16 && !strips_ge(65) && ktiles < 32) {
     cfg = kG1x1W16U2;
     splits = 1;
-  } else if (M >= 5 && M <= 16 && p.splits == 1 && strips_ge(513) && (spc == 3 || spc == 6 || spc == 7)) {
+  } else if (M >= 5 && M <= 16 && p.splits == 1 && strips_ge(513) &&
+             (spc == 3 || spc == 6 || spc == 7 || (spc == 5 && M >= 8))) {
     cfg = spc == 3 ? kG1x3W8U2 : spc == 7 ? kG1x7W8U1 : M >= 12 ? kG1x6W8U1 : kG1x3W8U2;
   } else if (M <= 4 && p.splits == 1 && !strips_ge(257) && ktiles < 128) {
     // Below 64 tiles the x copy (at most 4 rows of 63 * 256 bytes) fits.

@@ -173,7 +173,18 @@ GEMV_INT4_POLICY = [
     (1, 5120, 8192, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
     (2, 6144, 12288, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
     (2, 6144, 12288, True, "gemv 1x2 strips, 16 waves", 16, 32, 1),
-    (2, 5120, 25600, False, "gemv 1x2 strips, 16 waves", 16, 32, 1),
+    # ... from 128 tiles on 257..511 strips: x in LDS split 2-way (4-way from
+    # 192 tiles) at M <= 2, two strips per 8-wave workgroup split 4-way at M 3..4
+    (2, 5120, 25600, False, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 4),
+    (1, 5120, 17408, True, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 2),
+    (4, 5120, 25600, True, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    # M 3..4 on <= 128 strips from 64 tiles: two strips, 4-way split
+    (4, 2048, 11008, False, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    # M 3..4 on >= 1024 strips from 16 tiles: two strips per 8-wave workgroup
+    (4, 32768, 2048, False, "gemv 1x2 strips, 8 waves", 16, 32, 1),
+    # M 8..16 at five strips per CU: three strips per workgroup, six from M 12
+    (8, 19456, 2560, False, "gemv 1x3 strips, 8 waves", 16, 48, 1),
+    (16, 19456, 2560, True, "gemv 1x6 strips, 8 waves", 16, 96, 1),
     # M 3..4, >= 640 strips: x in LDS (int8 takes two strips per workgroup)
     (4, 12288, 4096, True, "gemv 1x1 strips, 8 waves, x in LDS", 16, 16, 1),
     # M 8..16, >= 2048 strips: four strips per 8-wave workgroup, or three /
