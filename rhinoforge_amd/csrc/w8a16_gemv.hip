@@ -1197,7 +1197,8 @@ GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
 //     (Qwen2.5-VL-3B down at M 16: 10.2 against 11.3 us with four strips);
 //     on 129..256 strips at M 5..6: one strip per 16-wave workgroup, no
 //     split (Qwen3-8B down at M 5: 10.8 against 11.7 us with two strips and
-//     two splits);
+//     two splits), and from M 8 three strips split 4-way where 4 x the
+//     workgroups of three strips fit one round of 256;
 //   * M 5..16 on <= 64 strips: one strip per 16-wave workgroup and no K
 //     split, or at M >= 8 from K 5120 one per 8-wave workgroup and a 4-way
 //     split (Pi0.5 expert o 1024 x 2048 at M 8: 3.8 against 5.9 us with
@@ -1263,6 +1264,14 @@ static bool plan_int8_rules(int M, int nstrips, int kblocks, int cu, int* cfg, i
     }
     if (M <= 6) {
       *cfg = kG1x1W16U2;
+      return true;
+    }
+    if (M >= 8 && (int64_t)groups(3) * 4 <= cu) {
+      // three strips split 4-way where that stays within one round
+      // (Qwen3-4B down 2560 x 9728 at M 8 / 16: 9.4 / 10.8 against 10.1 /
+      // 11.6 us with two strips split 2-way)
+      *cfg = kG1x3W8U2;
+      *splits = 4;
       return true;
     }
     return false;

@@ -92,6 +92,8 @@ GEMV_POLICY = [
     (7, 2056, 8200, "gemv 1x2 strips, 8 waves", 16, 32, 2),     # ragged N and K
     # M 5..6 (int8): one strip per 16-wave workgroup, no split
     (5, 2056, 8200, "gemv 1x1 strips, 16 waves", 16, 16, 1),
+    # from M 8 on <= 192 strips (int8): three strips split 4-way
+    (8, 2560, 9728, "gemv 1x3 strips, 8 waves", 16, 48, 4),
     # M 5..16, K 8192..16383, up to 128 strips (int8): two strips, 4-way K split
     (16, 1024, 8192, "gemv 1x2 strips, 8 waves", 16, 32, 4),
     # M 5..16 from K 16384 (int8): 4-way K split with five strips per
