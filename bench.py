@@ -603,12 +603,13 @@ MODEL_SHAPES = [
     ("Pi0.5 expert", "qkv", [2048, 256, 256], 1024), ("Pi0.5 expert", "o", [1024], 2048),
     ("Pi0.5 expert", "gate_up", [4096, 4096], 1024), ("Pi0.5 expert", "down", [1024], 4096),
 ]
-MODEL_SHAPES_M = (1, 4, 8, 16)
+MODEL_SHAPES_M = (1, 4, 8, 16, 24, 32)
 
 
 def bench_model_shapes(torch, rf):
-    """Per-launch times of MODEL_SHAPES at M in MODEL_SHAPES_M through
-    linear_into / linear_multi (AUTO), replayed from a HIP graph, rotating
+    """Per-launch times of MODEL_SHAPES at M in MODEL_SHAPES_M (decode sizes
+    and the GEMV / GEMM crossover) through linear_into / linear_multi
+    (AUTO), replayed from a HIP graph, rotating
     weight copies of >= 320 MB per shape (random int8 tiles: the timing does
     not depend on the values), against HBM."""
     from rhinoforge_amd import capi
