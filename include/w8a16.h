@@ -71,9 +71,10 @@ typedef enum rf_w8a16_status {
 
 /* Kernel choice (the analogue of `force_gemm`, rpu_linear.cpp:1094-1103). */
 #define RF_W8A16_KERNEL_AUTO 0
-#define RF_W8A16_KERNEL_GEMV 1 /* decode GEMV / skinny GEMM, M <= 64 (AUTO: M <= 16, M <= 28
-                                  with N*K <= 2^24, M <= 32 with N*K <= 2^23;
-                                  W4A16: M <= 64)                             */
+#define RF_W8A16_KERNEL_GEMV 1 /* decode GEMV / skinny GEMM, M <= 64 (AUTO: M <= 16, M <= 24
+                                  with N*K < 2^25, M <= 28 with N*K <= 2^24,
+                                  M <= 32 with N*K <= 2^23 or N <= 2048 and
+                                  N*K <= 2^24; W4A16: M <= 64)                */
 #define RF_W8A16_KERNEL_GEMM 2 /* prefill GEMM: x tiles staged in LDS by DMA, int8 weight
                                   tiles dequantized into fp16 MFMA operands (from
                                   registers on the large tiles, from LDS on the others) */
