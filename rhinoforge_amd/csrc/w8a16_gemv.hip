@@ -1194,7 +1194,13 @@ GemvPlan plan_gemv_int4(int M, const int* Ns, int nproj, int K, bool grouped,
 //     strips and 8 splits), four strips on 129..256 (Qwen2.5-VL-7B down at
 //     M 16: 16.6 against 21.5 us), two on fewer;
 //   * M 5..16, K 8192..16383, up to 128 strips: two strips, 4-way K split
-//     (Qwen2.5-VL-3B down at M 16: 10.2 against 11.3 us with four strips);
+//     (Qwen2.5-VL-3B down at M 16: 10.2 against 11.3 us with four strips),
+//     one strip per 8-wave workgroup split 2-way up to M 6 (M 8 below
+//     K 10240); on 257..511 strips from M 8 three strips split 2-way, or
+//     five split 4-way from K 10240 and M 12 where that fits one round of
+//     workgroups (from M 12 also at K 8192);
+//   * M 13..16 on 65..128 strips at K 5120..8191: two strips per 16-wave
+//     workgroup split 4-way;
 //     on 129..256 strips at M 5..6: one strip per 16-wave workgroup, no
 //     split (Qwen3-8B down at M 5: 10.8 against 11.7 us with two strips and
 //     two splits), and from M 8 three strips split 4-way where 4 x the
@@ -1255,11 +1261,25 @@ static bool plan_int8_rules(int M, int nstrips, int kblocks, int cu, int* cfg, i
     *splits = 4;
     return true;
   }
-  if (strips_ge(257)) return false;
+  if (strips_ge(257)) {
+    // K 8192..16383 from M 8: three strips split 2-way, or from K 10240 and
+    // M 12 five strips split 4-way (Qwen3-VL-32B o 5120 x 8192 at M 16: 12.5
+    // against 13.3 us; 5120 x 10240 at M 16: 14.3 against 16.6 us)
+    if (kblocks >= 128 && M >= 8 && (kblocks >= 160 || M >= 12)) {
+      const bool five = kblocks >= 160 && M >= 12 && (int64_t)groups(5) * 4 <= cu;
+      *cfg = five ? kG1x5W8U1 : kG1x3W8U2;
+      *splits = five ? 4 : 2;
+      return true;
+    }
+    return false;
+  }
   if (kblocks >= 128) {
     if (!strips_ge(129)) {
-      *cfg = kG1x2W8U2;
-      *splits = 4;
+      // (up to M 6, and M 8 below K 10240, one strip per 8-wave workgroup
+      // split 2-way: 2048 x 8192 at M 8 7.7 against 8.6 us)
+      const bool one = M <= 6 || (M <= 8 && kblocks < 160);
+      *cfg = one ? kG1x1W8U4 : kG1x2W8U2;
+      *splits = one ? 2 : 4;
       return true;
     }
     if (M <= 6) {
@@ -1275,6 +1295,13 @@ static bool plan_int8_rules(int M, int nstrips, int kblocks, int cu, int* cfg, i
       return true;
     }
     return false;
+  }
+  if (M >= 13 && kblocks >= 80 && strips_ge(65) && !strips_ge(129)) {
+    // two strips per 16-wave workgroup split 4-way (Qwen3-1.7B down 2048 x
+    // 6144 at M 16: 8.3 against 8.8 us)
+    *cfg = kG1x2W16U2;
+    *splits = 4;
+    return true;
   }
   if (!strips_ge(65)) {
     const bool split = M >= 8 && kblocks >= 80;

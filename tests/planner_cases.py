@@ -96,6 +96,19 @@ GEMV_POLICY = [
     (8, 2560, 9728, "gemv 1x3 strips, 8 waves", 16, 48, 4),
     # M 5..16, K 8192..16383, up to 128 strips (int8): two strips, 4-way K split
     (16, 1024, 8192, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    (8, 1536, 11008, "gemv 1x2 strips, 8 waves", 16, 32, 4),
+    # ... up to M 6 (M 8 below K 10240): one strip per 8-wave workgroup, 2-way split
+    (5, 2048, 11008, "gemv 1x1 strips, 8 waves", 16, 16, 2),
+    (8, 2048, 8192, "gemv 1x1 strips, 8 waves", 16, 16, 2),
+    # 257..511 strips at K 8192..16383 from M 8 (int8): three strips split
+    # 2-way; five split 4-way from K 10240 and M 12 where one round holds them
+    (16, 5120, 8192, "gemv 1x3 strips, 8 waves", 16, 48, 2),
+    (8, 5120, 10240, "gemv 1x3 strips, 8 waves", 16, 48, 2),
+    (12, 5120, 10240, "gemv 1x5 strips, 8 waves", 16, 80, 4),
+    (12, 6144, 10240, "gemv 1x3 strips, 8 waves", 16, 48, 2),
+    # M 13..16 on 65..128 strips at K 5120..8191 (int8): two strips per
+    # 16-wave workgroup, 4-way split
+    (16, 2048, 6144, "gemv 1x2 strips, 16 waves", 16, 32, 4),
     # M 5..16 from K 16384 (int8): 4-way K split with five strips per
     # workgroup on 257..511 strips, four on 129..256, two on fewer
     (16, 4112, 16456, "gemv 1x5 strips, 8 waves", 16, 80, 4),  # ragged N and K
